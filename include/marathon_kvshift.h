@@ -1,0 +1,192 @@
+/*
+ * marathon_kvshift.h -- C ABI of the MI355X (gfx950) KV-shift library.
+ *
+ * The library moves reused spans of cached K/V into a paged KV cache.  For every
+ * (layer, token, KV head) row it reads K[head_size] and V[head_size] from the source,
+ * re-rotates K by the span's token offset delta with NeoX rotate-half RoPE
+ *
+ *     out[i] = RN(RN(k[i] * cos[i]) + RN(k[partner(i)] * sgn[i]))       (fp32, no FMA)
+ *     partner(i) = i + rotary/2 (i < rotary/2),  i - rotary/2 (rotary/2 <= i < rotary)
+ *     sgn[i]     = -sin(a[i mod rotary/2]) (i < rotary/2),  +sin(...) (otherwise)
+ *     a[f]       = fl32((float)delta * inv_freq[f])
+ *
+ * rounds K back to the cache element type (RNE), copies V bit for bit, and writes the
+ * row at its destination slot (block = slot / block_size, offset = slot % block_size).
+ * Dimensions at or above `rotary`, and every element of a delta == 0 span, are copied
+ * bit for bit.  cos/sin are the fp32-rounded values of the exact cosine and sine of the
+ * fp32 angle (evaluated in double precision on the device).
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers named "device" are HIP device addresses; nothing is allocated and
+ *     nothing is synchronised.  Work is enqueued on `stream` (a hipStream_t; NULL is
+ *     the legacy default stream) and the call returns as soon as it is enqueued.
+ *   - Strides are in ELEMENTS of the cache element type.  16-byte alignment of every
+ *     base address and of every stride in bytes is required (MKV_ERR_ALIGN otherwise).
+ *   - Every slot, block id and block-table index is bounds-checked on the device
+ *     against the capacities given here; a row that fails is not read or written and,
+ *     when `error_flags` is non-NULL, sets MKV_FLAG_* bits there (atomic OR).
+ *   - Return value: MKV_OK or one of the MKV_ERR_* codes below; on error nothing was
+ *     enqueued.  mkv_last_error() returns a human-readable reason for the last error
+ *     raised on the calling thread.
+ *
+ * Element types (`dtype`): bf16, fp16 and fp32 rotate in fp32 and round to nearest
+ * even (NaN -> canonical quiet NaN); fp8 e4m3fn (OCP, max 448) dequantises K with the
+ * per-layer scale, rotates in fp32 and requantises:
+ *     x = fl32(decode(code) * k_scale[layer]);   y = rotation of x as above;
+ *     q = e4m3fn_RNE(clamp(fl32(y / k_scale[layer]), -448, 448))   (NaN -> 0x7F)
+ * V bytes are copied raw for every element type.
+ */
+#ifndef MARATHON_KVSHIFT_H
+#define MARATHON_KVSHIFT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------- */
+#define MKV_OK 0
+#define MKV_ERR_ARG 1         /* geometry or argument rejected (row size, rotary, NULL) */
+#define MKV_ERR_DTYPE 2       /* unknown element type */
+#define MKV_ERR_ALIGN 3       /* a base address or byte stride is not 16-byte aligned */
+#define MKV_ERR_UNSUPPORTED 4 /* geometry outside what the kernels handle */
+#define MKV_ERR_HIP 5         /* the HIP runtime refused the launch */
+
+/* ---- device error flags (bits OR-ed into *error_flags) ---------------------------- */
+#define MKV_FLAG_SRC_RANGE 1  /* a source slot / block id / table index out of range */
+#define MKV_FLAG_DST_RANGE 2  /* a destination slot / block id / table index out of range */
+#define MKV_FLAG_SPAN 4       /* a span with n_tokens < 0 or a group id out of range */
+#define MKV_FLAG_ALIGN 8      /* a base address from a k_base/v_base table not 16-byte aligned */
+
+/* ---- element types ---------------------------------------------------------------- */
+#define MKV_BF16 0
+#define MKV_F16 1
+#define MKV_F32 2
+#define MKV_FP8_E4M3 3
+
+/* ---- how one side maps a token position to a slot -------------------------------- */
+#define MKV_ADDR_FLAT 0  /* slot = position (a position-indexed store, block_size 1) */
+#define MKV_ADDR_SLOTS 1 /* slot = ((const int64_t*)index)[span.*_index + i] */
+#define MKV_ADDR_TABLE 2 /* slot = tbl[span.*_index + pos / bs] * bs + pos % bs,
+                            tbl = (const int32_t*)index, pos = span.*_pos + i */
+
+/* Limits of the batched entry point. */
+#define MKV_MAX_SPANS 4096
+#define MKV_MAX_HEAD_SIZE 512
+
+/*
+ * One reused span: n_tokens consecutive tokens whose K moves by `delta` positions.
+ * Token i of the span is read at source position src_pos + i and written at
+ * destination position dst_pos + i (FLAT/TABLE), or through the slot arrays at
+ * src_index + i / dst_index + i (SLOTS).  src_group / dst_group select the row of the
+ * side's base-address tables (for example the session whose store holds the span).
+ * 48 bytes, naturally aligned; arrays of it are read by the device.
+ */
+typedef struct mkv_span {
+  int64_t src_pos;
+  int64_t dst_pos;
+  int64_t src_index;
+  int64_t dst_index;
+  int32_t n_tokens;
+  int32_t delta;
+  int32_t src_group;
+  int32_t dst_group;
+} mkv_span_t;
+
+/*
+ * One side (source or destination) of a batched shift.
+ *   k_base, v_base : device arrays [groups * layers] of byte addresses of element 0 of
+ *                    K and V for (group, layer), row-major in group.  For the fused
+ *                    [..., 2 * head_size] layout v_base = k_base + head_size elements.
+ *   index          : device int64 slots (SLOTS) or int32 block ids (TABLE); NULL (FLAT).
+ *   index_len      : number of entries in `index`.
+ *   num_slots      : slots one (group, layer) buffer holds: blocks * block_size, or
+ *                    rows for FLAT.
+ *   group_slots    : optional device int64 [groups]: per-group num_slots (groups whose
+ *                    buffers differ in size, e.g. sessions' stores); NULL = num_slots.
+ *   block_stride, head_stride, offset_stride : element strides of (block, head,
+ *                    in-block offset).  FLAT uses block_size 1 and block_stride = the
+ *                    token stride.
+ */
+typedef struct mkv_side {
+  const uint64_t* k_base;
+  const uint64_t* v_base;
+  const void* index;
+  const int64_t* group_slots;
+  int64_t index_len;
+  int64_t num_slots;
+  int64_t block_stride;
+  int64_t head_stride;
+  int64_t offset_stride;
+  int32_t block_size;
+  int32_t mode;
+  int32_t groups;
+  int32_t reserved;
+} mkv_side_t;
+
+/*
+ * A batched shift: every span x every layer in ONE launch.
+ *   spans     : device [n_spans], 0 <= n_spans <= MKV_MAX_SPANS.
+ *   inv_freq  : device fp32 [rotary / 2]; may be NULL when rotary == 0.
+ *   k_scale   : device fp32 [layers], fp8 only (NULL otherwise).
+ *   error_flags : device int32 [1] or NULL.
+ */
+typedef struct mkv_shift_desc {
+  const mkv_span_t* spans;
+  const float* inv_freq;
+  const float* k_scale;
+  int32_t* error_flags;
+  int32_t n_spans;
+  int32_t layers;
+  int32_t heads;
+  int32_t head_size;
+  int32_t rotary;
+  int32_t dtype;
+  mkv_side_t src;
+  mkv_side_t dst;
+} mkv_shift_desc_t;
+
+/*
+ * Single span, single layer: the drop-in for
+ *   scatter_shifted(src, kv, slots, block_size, hnd, shift)
+ *   (src/marathon/shift_kernels.py:166-210; its Triton kernel :89-132 and its torch
+ *   path :141-159).
+ * src       : device [n_tokens, heads, 2 * head_size] rows with the given token/head
+ *             strides (K in [..., :head_size], V in [..., head_size:]).
+ * kv        : device fused paged cache; (block, head, offset) strides select HND
+ *             [blocks, heads, bs, 2D] or NHD [blocks, bs, heads, 2D]
+ *             (shift_kernels.py:135-138).  kv_num_blocks bounds the slots.
+ * slots     : device int64 [n_tokens] flat destination slots (shift_store.py:56-60).
+ * inv_freq, rotary, delta : the rotation (rope_shift, shift_kernels.py:68-84);
+ *             delta == 0 or rotary == 0 is a plain scatter.  n_tokens == 0 is a no-op.
+ * k_scale   : device fp32 [1] for MKV_FP8_E4M3, else NULL.
+ */
+int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_head_stride,
+                        void* kv, int64_t kv_block_stride, int64_t kv_head_stride,
+                        int64_t kv_offset_stride, int64_t kv_num_blocks,
+                        const int64_t* slots, int64_t n_tokens, int32_t heads,
+                        int32_t head_size, int32_t block_size, int32_t dtype,
+                        const float* inv_freq, int32_t rotary, int32_t delta,
+                        const float* k_scale, int32_t* error_flags, void* stream);
+
+/*
+ * Batched multi-span, multi-layer, multi-session shift in one launch: replaces the
+ * connector's per-load, per-layer loop of store.read + scatter_shifted
+ * (src/marathon/vllm_shift_connector.py:481-534, loop at :505-518) and the HF
+ * prototype's per-segment stitch (src/marathon/kvshift.py:242-268, :265-266).
+ */
+int mkv_shift_spans(const mkv_shift_desc_t* desc, void* stream);
+
+/* Human-readable reason for the last non-MKV_OK return on this thread ("" if none). */
+const char* mkv_last_error(void);
+
+/* ABI version of this header: (major << 16) | minor. */
+int32_t mkv_abi_version(void);
+#define MKV_ABI_VERSION ((1 << 16) | 0)
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MARATHON_KVSHIFT_H */

@@ -1,0 +1,227 @@
+"""Fused re-rotate-and-scatter on MI355X: the host API of src/marathon/shift_kernels.py.
+
+Same names, argument meanings and error behaviour as the reference module:
+
+* :class:`RopeShift` / :func:`rope_shift` -- per-delta rotation tables
+  (shift_kernels.py:50-84).  The tables are kept for callers that read them; the HIP
+  kernel itself only needs ``delta`` and ``inv_freq`` and evaluates cos/sin per span
+  on the device.
+* :func:`scatter_shifted` -- write ``src`` ``[n, heads, 2*head_size]`` into the paged
+  ``kv`` at ``slots``, K re-rotated by delta, V copied bit for bit
+  (shift_kernels.py:166-210).  One call is one HIP launch on the current stream.
+* :func:`use_hip` -- the analogue of ``use_triton`` (shift_kernels.py:162-163).
+* :func:`warmup` -- kept for the connector's call (vllm_shift_connector.py:404-405);
+  the kernels are compiled ahead of time, so it only loads the library.
+
+Divergence, on purpose: there is no torch fallback.  The reference's
+``scatter_shifted`` falls back to ``scatter_shifted_torch`` off-GPU
+(shift_kernels.py:180-181); here a tensor that is not on a HIP device raises, so a
+measurement or a parity check can never run anything but the HIP kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.bfloat16: _lib.MKV_BF16,
+    torch.float16: _lib.MKV_F16,
+    torch.float32: _lib.MKV_F32,
+    torch.float8_e4m3fn: _lib.MKV_FP8_E4M3,
+}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported KV cache dtype {dtype}") from None
+
+
+@dataclass(frozen=True)
+class RopeShift:
+    """Rotation for one delta on one device (shift_kernels.py:50-65).
+
+    ``cos``/``sgn`` fp32 [head_size], ``partner`` int32 [head_size], ``emb_cos`` /
+    ``emb_sin`` fp32 [rotary]: the same tables the reference builds.  ``inv_freq`` is the
+    fp32 [rotary / 2] vector the kernel reads; ``rotary`` is 2 * len(inv_freq).
+    """
+
+    delta: int
+    cos: torch.Tensor
+    sgn: torch.Tensor
+    partner: torch.Tensor
+    emb_cos: torch.Tensor
+    emb_sin: torch.Tensor
+    inv_freq: torch.Tensor
+    rotary: int
+
+
+def inv_freq_for(head_dim: int, rope_theta: float, partial_rotary_factor: float = 1.0) -> torch.Tensor:
+    """The connector's inverse frequencies (vllm_shift_connector.py:194-199), fp32, CPU."""
+    rotary = int(head_dim * partial_rotary_factor)
+    return 1.0 / (float(rope_theta) ** (torch.arange(0, rotary, 2, dtype=torch.float32) / rotary))
+
+
+def rope_shift(delta: int, head_size: int, inv_freq: torch.Tensor, device) -> RopeShift:
+    """Tables that move RoPE'd keys ``delta`` positions (shift_kernels.py:68-84).
+
+    cos/sin are the exact values of the fp32 angles ``fl32(delta * inv_freq)`` rounded
+    once to fp32 -- the same numbers the kernel computes on the device.
+    """
+    rotary = 2 * int(inv_freq.numel())
+    assert rotary <= head_size, f"rotary {rotary} > head_size {head_size}"
+    half = rotary // 2
+    inv = inv_freq.detach().to(device="cpu", dtype=torch.float32).numpy()
+    ang = (np.float32(delta) * inv).astype(np.float64)
+    c = np.cos(ang).astype(np.float32)
+    s = np.sin(ang).astype(np.float32)
+    emb_c = np.concatenate((c, c))
+    emb_s = np.concatenate((s, s))
+    cos = np.ones(head_size, np.float32)
+    sgn = np.zeros(head_size, np.float32)
+    cos[:rotary] = emb_c
+    sgn[:half] = -emb_s[:half]
+    sgn[half:rotary] = emb_s[half:rotary]
+    partner = np.arange(head_size, dtype=np.int32)
+    partner[:half] += half
+    partner[half:rotary] -= half
+
+    def dev(a):
+        return torch.from_numpy(a).to(device)
+
+    return RopeShift(
+        int(delta),
+        dev(cos),
+        dev(sgn),
+        dev(partner),
+        dev(emb_c),
+        dev(emb_s),
+        dev(inv.copy()),
+        rotary,
+    )
+
+
+def use_hip(kv: torch.Tensor) -> bool:
+    """True when ``kv`` lives on a HIP device, i.e. when :func:`scatter_shifted` runs."""
+    return bool(kv.is_cuda)
+
+
+def paged_strides(kv: torch.Tensor, hnd: bool) -> tuple[int, int, int]:
+    """(block, head, in-block offset) element strides of a fused 4-D cache.
+
+    HND ``[blocks, heads, bs, 2D]`` or NHD ``[blocks, bs, heads, 2D]``
+    (shift_kernels.py:135-138).
+    """
+    s = kv.stride()
+    return (s[0], s[1], s[2]) if hnd else (s[0], s[2], s[1])
+
+
+def current_stream(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _scale_tensor(k_scale, device) -> torch.Tensor:
+    if isinstance(k_scale, torch.Tensor):
+        t = k_scale.detach().reshape(-1)[:1]
+        if t.device != device or t.dtype != torch.float32:
+            t = t.to(device=device, dtype=torch.float32)
+        return t.contiguous()
+    return torch.tensor([float(k_scale)], dtype=torch.float32, device=device)
+
+
+def scatter_shifted(
+    src: torch.Tensor,
+    kv: torch.Tensor,
+    slots: torch.Tensor,
+    block_size: int,
+    hnd: bool,
+    shift: RopeShift | None,
+    *,
+    k_scale=None,
+    error_flags: torch.Tensor | None = None,
+) -> None:
+    """Write ``src`` (``[n, heads, 2*head_size]``) into ``kv``'s slots, K rotated by delta.
+
+    ``slots`` are flat destination slots (block ``slot // block_size``, offset
+    ``slot % block_size``); ``hnd`` selects the paged layout; ``shift`` of ``None`` (or
+    delta 0) is a plain scatter (shift_kernels.py:166-179).  Asynchronous on the
+    current stream.  ``k_scale`` (fp8 caches only) is the layer's K scale;
+    ``error_flags`` an optional int32 device tensor that collects out-of-range bits.
+    """
+    if not use_hip(kv):
+        raise RuntimeError(
+            "scatter_shifted: kv is not on a HIP device; marathon_amd has no CPU path"
+        )
+    n, heads, two_d = src.shape
+    d = two_d // 2
+    assert kv.shape[-1] == two_d, f"src row {two_d} != kv row {kv.shape[-1]}"
+    if n == 0:
+        return
+    if src.dtype != kv.dtype:
+        raise TypeError(f"src dtype {src.dtype} != kv dtype {kv.dtype}")
+    if src.device != kv.device:
+        raise ValueError(f"src on {src.device}, kv on {kv.device}")
+    if src.stride(2) != 1 or kv.stride(3) != 1:
+        raise ValueError("src and kv rows must be contiguous in the last dimension")
+    code = dtype_code(kv.dtype)
+    if slots.device != kv.device or slots.dtype != torch.int64 or not slots.is_contiguous():
+        slots = slots.to(device=kv.device, dtype=torch.int64, non_blocking=True).contiguous()
+    if slots.numel() != n:
+        raise ValueError(f"{slots.numel()} slots for {n} tokens")
+    rotate = shift is not None and shift.delta != 0 and shift.rotary > 0
+    inv = None
+    scale = None
+    if rotate:
+        inv = shift.inv_freq
+        if inv.device != kv.device:
+            inv = inv.to(kv.device)
+        if code == _lib.MKV_FP8_E4M3:
+            if k_scale is None:
+                raise ValueError("fp8 KV cache needs k_scale")
+            scale = _scale_tensor(k_scale, kv.device)
+    blk_s, head_s, off_s = paged_strides(kv, hnd)
+    with torch.cuda.device(kv.device):
+        rc = _lib.lib().mkv_scatter_shifted(
+            src.data_ptr(),
+            src.stride(0),
+            src.stride(1),
+            kv.data_ptr(),
+            blk_s,
+            head_s,
+            off_s,
+            kv.shape[0],
+            slots.data_ptr(),
+            n,
+            heads,
+            d,
+            int(block_size),
+            code,
+            _ptr(inv),
+            shift.rotary if rotate else 0,
+            shift.delta if rotate else 0,
+            _ptr(scale),
+            _ptr(error_flags),
+            ctypes.c_void_p(current_stream(kv.device)),
+        )
+    _lib.check(rc)
+
+
+def warmup(kv: torch.Tensor, block_size: int, hnd: bool) -> None:
+    """Load the library before the first real load (shift_kernels.py:213-238).
+
+    The reference pre-compiles its Triton specialisations here; HIP kernels are
+    compiled ahead of time, so there is nothing to compile -- only the library load.
+    """
+    if use_hip(kv):
+        _lib.lib()

@@ -1,0 +1,238 @@
+"""Batched shifts: every span x every layer x every session in ONE HIP launch.
+
+The reference issues one Triton launch per layer per load
+(src/marathon/vllm_shift_connector.py:505-515) and the HF prototype one rotation per
+layer per segment (src/marathon/kvshift.py:242-268).  Here a :class:`ShiftPlan` holds a
+device-resident span table (``mkv_span_t``), per-(group, layer) base-address tables for
+source and destination, and the slot/block-table arrays, and :meth:`ShiftPlan.launch`
+enqueues the whole shift as one ``mkv_shift_spans`` call.
+
+Caches are described by :class:`CacheSet`: ``caches[group][layer]`` tensors of one
+layout -- ``flat`` ``[rows, heads, 2D]`` (a position-indexed store, the reference's
+``ShiftStore`` buffer, shift_store.py:225-236), or paged ``hnd`` ``[blocks, heads, bs,
+2D]`` / ``nhd`` ``[blocks, bs, heads, 2D]`` (vLLM's fused layouts,
+vllm_shift_connector.py:396-402).  A group is whatever owns a buffer: a session's store,
+or the one shared paged cache.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .shift_kernels import current_stream, dtype_code
+
+MODES = {"flat": _lib.MKV_ADDR_FLAT, "slots": _lib.MKV_ADDR_SLOTS, "table": _lib.MKV_ADDR_TABLE}
+
+
+@dataclass
+class CacheSet:
+    """``caches[group][layer]`` of one layout; every tensor has the same trailing shape,
+    strides and dtype (groups may differ in their number of blocks / rows)."""
+
+    caches: list
+    layout: str  # "flat" | "hnd" | "nhd"
+    block_size: int = 1
+
+    def __post_init__(self):
+        if self.layout not in ("flat", "hnd", "nhd"):
+            raise ValueError(f"layout {self.layout!r}")
+        if not self.caches or not self.caches[0]:
+            raise ValueError("empty CacheSet")
+        if isinstance(self.caches[0], torch.Tensor):
+            self.caches = [list(self.caches)]
+        first = self.caches[0][0]
+        want_dim = 3 if self.layout == "flat" else 4
+        for row in self.caches:
+            if len(row) != len(self.caches[0]):
+                raise ValueError("every group needs the same number of layers")
+            for t in row:
+                if t.dim() != want_dim:
+                    raise ValueError(f"{self.layout} cache must be {want_dim}-D, got {tuple(t.shape)}")
+                if t.dtype != first.dtype or t.device != first.device:
+                    raise ValueError("caches differ in dtype or device")
+                if t.shape[1:] != first.shape[1:] or t.stride() != first.stride():
+                    raise ValueError("caches differ in trailing shape or strides")
+                if t.stride(-1) != 1:
+                    raise ValueError("rows must be contiguous in the last dimension")
+        if self.layout == "flat":
+            self.block_size = 1
+        elif self.layout == "hnd" and first.shape[2] != self.block_size:
+            raise ValueError(f"HND cache block dim {first.shape[2]} != block_size {self.block_size}")
+        elif self.layout == "nhd" and first.shape[1] != self.block_size:
+            raise ValueError(f"NHD cache block dim {first.shape[1]} != block_size {self.block_size}")
+
+    @property
+    def groups(self) -> int:
+        return len(self.caches)
+
+    @property
+    def layers(self) -> int:
+        return len(self.caches[0])
+
+    @property
+    def first(self) -> torch.Tensor:
+        return self.caches[0][0]
+
+    @property
+    def heads(self) -> int:
+        return self.first.shape[1] if self.layout in ("flat", "hnd") else self.first.shape[2]
+
+    @property
+    def head_size(self) -> int:
+        return self.first.shape[-1] // 2
+
+    @property
+    def strides(self) -> tuple[int, int, int]:
+        s = self.first.stride()
+        if self.layout == "flat":
+            return s[0], s[1], 0
+        return (s[0], s[1], s[2]) if self.layout == "hnd" else (s[0], s[2], s[1])
+
+    def slots_of(self, t: torch.Tensor) -> int:
+        return t.shape[0] * (1 if self.layout == "flat" else self.block_size)
+
+
+class ShiftPlan:
+    """A batched shift, resident on the device and launchable any number of times.
+
+    ``spans``: a ``SPAN_DTYPE`` structured array (or anything ``np.asarray`` turns into
+    one).  ``src_index`` / ``dst_index``: int64 slots (mode ``slots``), int32 block ids
+    (mode ``table``) or ``None`` (mode ``flat``).  ``inv_freq``: fp32 [rotary / 2].
+    ``k_scale``: fp32 [layers] for fp8 caches.
+    """
+
+    def __init__(
+        self,
+        spans,
+        src: CacheSet,
+        dst: CacheSet,
+        *,
+        inv_freq: torch.Tensor | None,
+        src_mode: str = "flat",
+        src_index: torch.Tensor | None = None,
+        dst_mode: str = "slots",
+        dst_index: torch.Tensor | None = None,
+        k_scale: torch.Tensor | None = None,
+    ):
+        spans = np.ascontiguousarray(np.asarray(spans, dtype=_lib.SPAN_DTYPE))
+        if src.layers != dst.layers:
+            raise ValueError(f"src has {src.layers} layers, dst {dst.layers}")
+        if src.first.dtype != dst.first.dtype:
+            raise TypeError("src and dst dtypes differ")
+        if (src.heads, src.head_size) != (dst.heads, dst.head_size):
+            raise ValueError("src and dst geometry differ")
+        self.device = dst.first.device
+        if src.first.device != self.device:
+            raise ValueError("src and dst on different devices")
+        self.src, self.dst = src, dst
+        self.n_spans = int(spans.shape[0])
+        self.tokens = int(np.maximum(spans["n_tokens"], 0).sum()) if self.n_spans else 0
+        self.dtype = dtype_code(dst.first.dtype)
+        self._keep: list = []
+        dev = self.device
+
+        def upload(a: np.ndarray) -> torch.Tensor:
+            t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+            self._keep.append(t)
+            return t
+
+        self.rotary = 0 if inv_freq is None else 2 * int(inv_freq.numel())
+        inv_dev = None
+        if inv_freq is not None:
+            inv_dev = inv_freq.detach().to(device=dev, dtype=torch.float32).contiguous()
+            self._keep.append(inv_dev)
+        scale_dev = None
+        if self.dtype == _lib.MKV_FP8_E4M3 and self.rotary:
+            if k_scale is None:
+                raise ValueError("fp8 caches need k_scale [layers]")
+            scale_dev = k_scale.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+            if scale_dev.numel() < dst.layers:
+                raise ValueError("k_scale needs one entry per layer")
+            self._keep.append(scale_dev)
+
+        src_side = self._side(src, src_mode, src_index, upload)
+        dst_side = self._side(dst, dst_mode, dst_index, upload)
+        span_bytes = upload(spans.view(np.uint8).reshape(-1)) if self.n_spans else None
+
+        self.descs = []
+        step = _lib.MKV_MAX_SPANS
+        for lo in range(0, self.n_spans, step):
+            cnt = min(step, self.n_spans - lo)
+            d = _lib.ShiftDesc()
+            d.spans = span_bytes.data_ptr() + lo * _lib.SPAN_DTYPE.itemsize
+            d.inv_freq = inv_dev.data_ptr() if inv_dev is not None else None
+            d.k_scale = scale_dev.data_ptr() if scale_dev is not None else None
+            d.error_flags = None
+            d.n_spans = cnt
+            d.layers = dst.layers
+            d.heads = dst.heads
+            d.head_size = dst.head_size
+            d.rotary = self.rotary
+            d.dtype = self.dtype
+            d.src = src_side
+            d.dst = dst_side
+            self.descs.append(d)
+
+    def _side(self, cs: CacheSet, mode: str, index, upload) -> _lib.Side:
+        if mode not in MODES:
+            raise ValueError(f"mode {mode!r}")
+        eb = cs.first.element_size()
+        hs = cs.head_size
+        k = np.array([[t.data_ptr() for t in row] for row in cs.caches], dtype=np.uint64)
+        v = k + np.uint64(hs * eb)
+        side = _lib.Side()
+        side.k_base = upload(k.reshape(-1).view(np.int64)).data_ptr()
+        side.v_base = upload(v.reshape(-1).view(np.int64)).data_ptr()
+        caps = np.array([cs.slots_of(row[0]) for row in cs.caches], dtype=np.int64)
+        side.num_slots = int(caps.min())
+        side.group_slots = None if np.all(caps == caps[0]) else upload(caps).data_ptr()
+        if mode == "flat":
+            side.index = None
+            side.index_len = 0
+        else:
+            if index is None:
+                raise ValueError(f"mode {mode!r} needs an index array")
+            want = torch.int64 if mode == "slots" else torch.int32
+            t = index.to(device=self.device, dtype=want).contiguous()
+            self._keep.append(t)
+            side.index = t.data_ptr() if t.numel() else None
+            side.index_len = t.numel()
+        bs, hstr, ostr = cs.strides
+        side.block_stride, side.head_stride, side.offset_stride = bs, hstr, ostr
+        side.block_size = cs.block_size
+        side.mode = MODES[mode]
+        side.groups = cs.groups
+        return side
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        """K and V read once and written once: 2 * tokens * layers * heads * 2D * elem."""
+        eb = self.dst.first.element_size()
+        return 2 * self.tokens * self.dst.layers * self.dst.heads * 2 * self.dst.head_size * eb
+
+    def launch(self, stream: int | None = None, error_flags: torch.Tensor | None = None) -> None:
+        """Enqueue the shift (one launch per 4096 spans) on ``stream`` (default: current)."""
+        if stream is None:
+            stream = current_stream(self.device)
+        L = _lib.lib()
+        with torch.cuda.device(self.device):
+            for d in self.descs:
+                d.error_flags = error_flags.data_ptr() if error_flags is not None else None
+                _lib.check(L.mkv_shift_spans(ctypes.byref(d), ctypes.c_void_p(stream)))
+
+
+def span_array(rows) -> np.ndarray:
+    """Build a ``SPAN_DTYPE`` array from dicts or tuples in field order."""
+    out = np.zeros(len(rows), dtype=_lib.SPAN_DTYPE)
+    for i, r in enumerate(rows):
+        if isinstance(r, dict):
+            for k, val in r.items():
+                out[i][k] = val
+        else:
+            out[i] = tuple(r)
+    return out

@@ -1,0 +1,44 @@
+"""The reference's torch shift path, run on the CPU -- TEST INFRASTRUCTURE ONLY.
+
+Restates the op sequence of ``scatter_shifted_torch`` (src/marathon/shift_kernels.py:
+141-159) with the tables of ``rope_shift`` (:68-84): slice K, upcast to fp32, build
+rotate_half with a ``cat``, ``k * emb_cos + rot * emb_sin`` as separate fp32 ops, cast
+back to the cache dtype, ``cat`` K and V, and scatter with advanced indexing.  It is
+kept op-for-op alike on purpose: it is the timed CPU baseline ("the reference's torch
+CPU shift path") and the "reference rotation" the kernels are held to within 1 ulp.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def rope_emb_tables(delta: int, inv_freq: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``emb_cos``/``emb_sin`` as rope_shift builds them on the CPU (shift_kernels.py:73, 83-84)."""
+    ang = float(delta) * inv_freq.to(dtype=torch.float32)
+    emb = torch.cat((ang, ang))
+    return emb.cos(), emb.sin()
+
+
+def shift_into_paged(
+    rows: torch.Tensor,
+    cache: torch.Tensor,
+    slot: torch.Tensor,
+    block_size: int,
+    hnd: bool,
+    emb: tuple[torch.Tensor, torch.Tensor] | None,
+) -> None:
+    """One layer of the torch path: rotate K of ``rows`` [n, heads, 2D] and scatter.
+
+    ``emb`` is ``(emb_cos, emb_sin)`` or ``None`` for a delta-0 plain scatter.
+    """
+    d = rows.shape[-1] // 2
+    keys = rows[..., :d]
+    if emb is not None:
+        kf = keys.to(torch.float32)
+        h = kf.shape[-1] // 2
+        rotated_half = torch.cat((-kf[..., h:], kf[..., :h]), dim=-1)
+        keys = (kf * emb[0] + rotated_half * emb[1]).to(cache.dtype)
+    block, offset = slot // block_size, slot % block_size
+    where = (block, slice(None), offset) if hnd else (block, offset)
+    cache[where] = torch.cat((keys, rows[..., d:]), dim=-1)

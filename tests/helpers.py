@@ -1,0 +1,57 @@
+"""Helpers shared by the tests: bit views, seeded inputs, oracle bridges."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import kvshift_oracle as orc
+
+TORCH_BITS = {
+    torch.bfloat16: (torch.int16, np.uint16, "bf16"),
+    torch.float16: (torch.int16, np.uint16, "f16"),
+    torch.float32: (torch.int32, np.uint32, "f32"),
+    torch.float8_e4m3fn: (torch.uint8, np.uint8, "fp8"),
+}
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """Raw bit patterns of a tensor (copied to the CPU)."""
+    iv, nv, _ = TORCH_BITS[t.dtype]
+    return t.detach().cpu().contiguous().view(iv).numpy().view(nv).copy()
+
+
+def dname(dtype: torch.dtype) -> str:
+    return TORCH_BITS[dtype][2]
+
+
+def inv_freq(rotary: int = 128, theta: float = 1e6) -> torch.Tensor:
+    """The reference tests' inverse frequencies (tests/test_shift_kernels.py:28-29)."""
+    return 1.0 / (theta ** (torch.arange(0, rotary, 2, dtype=torch.float32) / rotary))
+
+
+def randn(shape, dtype, gen, scale: float = 1.0) -> torch.Tensor:
+    if dtype == torch.float8_e4m3fn:
+        x = torch.randn(shape, dtype=torch.float32, generator=gen) / scale
+        return x.clamp(-448, 448).to(torch.float8_e4m3fn)
+    return torch.randn(shape, dtype=torch.float32, generator=gen).to(dtype)
+
+
+def oracle_side(cs, mode: str, index) -> orc.Side:
+    """An oracle Side holding CPU bit copies of a marathon_amd CacheSet."""
+    caches = [[bits(t) for t in row] for row in cs.caches]
+    idx = None if index is None else index.detach().cpu().numpy()
+    return orc.Side(caches, cs.layout, cs.block_size, mode, idx)
+
+
+def oracle_spans(spans: np.ndarray) -> list:
+    return [
+        orc.Span(int(r["src_pos"]), int(r["dst_pos"]), int(r["n_tokens"]), int(r["delta"]),
+                 int(r["src_index"]), int(r["dst_index"]), int(r["src_group"]),
+                 int(r["dst_group"]))
+        for r in spans
+    ]
+
+
+def ulp_bf16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    return orc.ulp_distance_bf16(a, b)

@@ -1,0 +1,148 @@
+"""The C ABI: the library loads, exports every declared symbol, its structs match the
+header, and its host-side argument checks answer without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from marathon_amd import _lib
+from marathon_amd.shift_kernels import rope_shift, scatter_shifted
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def _declared_functions() -> set[str]:
+    names = set()
+    for fn in os.listdir(INCLUDE):
+        if fn.endswith(".h"):
+            text = open(os.path.join(INCLUDE, fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names |= set(re.findall(r"\b(mkv_\w+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_function():
+    declared = _declared_functions()
+    assert declared == set(_lib.EXPORTED), declared
+    lib = _lib.lib()
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version():
+    assert _lib.lib().mkv_abi_version() == _lib.MKV_ABI_VERSION
+
+
+PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "marathon_kvshift.h"
+#define O(T, f) printf(#T "." #f " %zu\n", offsetof(T, f))
+int main(void) {
+  printf("span %zu side %zu desc %zu\n", sizeof(mkv_span_t), sizeof(mkv_side_t),
+         sizeof(mkv_shift_desc_t));
+  O(mkv_span_t, src_pos); O(mkv_span_t, dst_pos); O(mkv_span_t, src_index);
+  O(mkv_span_t, dst_index); O(mkv_span_t, n_tokens); O(mkv_span_t, delta);
+  O(mkv_span_t, src_group); O(mkv_span_t, dst_group);
+  O(mkv_side_t, k_base); O(mkv_side_t, v_base); O(mkv_side_t, index);
+  O(mkv_side_t, group_slots); O(mkv_side_t, index_len); O(mkv_side_t, num_slots);
+  O(mkv_side_t, block_stride); O(mkv_side_t, head_stride); O(mkv_side_t, offset_stride);
+  O(mkv_side_t, block_size); O(mkv_side_t, mode); O(mkv_side_t, groups);
+  O(mkv_shift_desc_t, spans); O(mkv_shift_desc_t, inv_freq); O(mkv_shift_desc_t, k_scale);
+  O(mkv_shift_desc_t, error_flags); O(mkv_shift_desc_t, n_spans); O(mkv_shift_desc_t, layers);
+  O(mkv_shift_desc_t, heads); O(mkv_shift_desc_t, head_size); O(mkv_shift_desc_t, rotary);
+  O(mkv_shift_desc_t, dtype); O(mkv_shift_desc_t, src); O(mkv_shift_desc_t, dst);
+  return 0;
+}
+"""
+
+
+def test_struct_layout_matches_the_header(tmp_path):
+    src = tmp_path / "probe.c"
+    src.write_text(PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c99", f"-I{INCLUDE}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    sizes = out[0].split()
+    assert int(sizes[1]) == ctypes.sizeof(_lib.Span)
+    assert int(sizes[3]) == ctypes.sizeof(_lib.Side)
+    assert int(sizes[5]) == ctypes.sizeof(_lib.ShiftDesc)
+    types = {"mkv_span_t": _lib.Span, "mkv_side_t": _lib.Side, "mkv_shift_desc_t": _lib.ShiftDesc}
+    for line in out[1:]:
+        if not line:
+            continue
+        key, off = line.split()
+        tname, field = key.split(".")
+        assert getattr(types[tname], field).offset == int(off), key
+    assert _lib.SPAN_DTYPE.itemsize == ctypes.sizeof(_lib.Span)
+    for name in _lib.SPAN_DTYPE.names:
+        assert _lib.SPAN_DTYPE.fields[name][1] == getattr(_lib.Span, name).offset
+
+
+def _scatter(**kw):
+    args = dict(src=1 << 20, sts=2048, shs=256, kv=1 << 24, kbs=32768, khs=4096, kos=256,
+                nblk=64, slots=1 << 21, n=8, heads=8, d=128, bs=16, dtype=_lib.MKV_BF16,
+                inv=1 << 22, rot=128, delta=5, scale=None, err=None)
+    args.update(kw)
+    return _lib.lib().mkv_scatter_shifted(*args.values(), None)
+
+
+def test_host_side_argument_errors_need_no_gpu():
+    lib = _lib.lib()
+    assert _scatter(dtype=9) == _lib.MKV_ERR_DTYPE
+    assert b"dtype" in lib.mkv_last_error()
+    assert _scatter(d=0) == _lib.MKV_ERR_UNSUPPORTED
+    assert _scatter(d=1024, rot=128) == _lib.MKV_ERR_UNSUPPORTED
+    assert _scatter(rot=256) == _lib.MKV_ERR_ARG  # rotary > head_size (shift_kernels.py:71)
+    assert _scatter(rot=72) == _lib.MKV_ERR_UNSUPPORTED  # not a multiple of 16 for bf16
+    assert _scatter(d=100) == _lib.MKV_ERR_UNSUPPORTED  # 200-byte head is not 16-byte sized
+    assert _scatter(heads=0) == _lib.MKV_ERR_ARG
+    assert _scatter(n=-1) == _lib.MKV_ERR_ARG
+    assert _scatter(src=None) == _lib.MKV_ERR_ARG
+    assert _scatter(inv=None) == _lib.MKV_ERR_ARG
+    assert _scatter(dtype=_lib.MKV_FP8_E4M3, scale=None) == _lib.MKV_ERR_ARG
+    assert _scatter(src=(1 << 20) + 8) == _lib.MKV_ERR_ALIGN
+    assert _scatter(sts=2047) == _lib.MKV_ERR_ALIGN
+    # the reference returns early on an empty load (shift_kernels.py:185-186)
+    assert _scatter(n=0) == _lib.MKV_OK
+    assert lib.mkv_last_error() == b""
+
+
+def test_batched_entry_point_argument_errors_need_no_gpu():
+    lib = _lib.lib()
+    assert lib.mkv_shift_spans(None, None) == _lib.MKV_ERR_ARG
+    d = _lib.ShiftDesc()
+    d.heads, d.head_size, d.rotary, d.dtype, d.layers = 8, 128, 128, _lib.MKV_BF16, 2
+    d.n_spans = 0
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_OK
+    d.n_spans = _lib.MKV_MAX_SPANS + 1
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
+    d.n_spans = 1
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG  # NULL spans
+    d.spans = 1 << 20
+    d.inv_freq = 1 << 21
+    d.src.mode = 7
+    d.src.block_size = 1
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    assert b"mode" in lib.mkv_last_error()
+
+
+def test_python_api_refuses_tensors_off_the_gpu():
+    src = torch.zeros(4, 8, 256, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 8, 16, 256, dtype=torch.bfloat16)
+    inv = 1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        scatter_shifted(src, kv, torch.arange(4), 16, True, rope_shift(3, 128, inv, "cpu"))
+
+
+def test_rope_shift_asserts_rotary_fits():
+    inv = torch.ones(80)
+    with pytest.raises(AssertionError, match="rotary 160 > head_size 128"):
+        rope_shift(1, 128, inv, "cpu")
