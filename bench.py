@@ -1,0 +1,285 @@
+"""Benchmark: fused KV-shift throughput on one MI355X.
+
+Workload (one "step" = one whole shift, one launch): the Qwen3-14B-shaped multi-span
+shift -- 40 layers, 8 KV heads, head_dim 128, bf16, a 30,720-token history with 8
+reused spans (seed 3: 22,141 tokens, deltas in [-2048, 2048] incl. 0, no boundary on a
+multiple of 16), read from the session store's block layout through a shuffled block
+table and written into an HND paged cache through a slot mapping.  Inputs are resident
+in HBM before timing.  Bytes are algorithmic: each K and V element read once and
+written once (2 * tokens * layers * 8 * 256 * 2 B), reported in decimal GB/s.
+
+Prints one JSON line.  Also measured, in the same line:
+* ``roofline``: bytes per launch / mean launch time from HIP events on the launch
+  stream, against the 8 TB/s HBM peak; ``traffic`` from the committed rocprofv3
+  FETCH_SIZE/WRITE_SIZE profile of this kernel and workload, when present.
+* ``cpu_baseline``: the reference's torch shift path (its op sequence, restated in
+  ``oracle/torch_path.py``) on the host CPU, on the Qwen3-0.6B-shaped config
+  (28 layers x 4,096 tokens, delta +37), best of 3 after a warmup.
+* ``reference_shape``: the reference benchmark's own shape (30,720 tokens x 40 layers,
+  delta 186, flat store -> HND paged cache, scattered block table), for comparison with
+  its published 6.54 ms on an RTX 5090.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_GBS = 8000.0  # MI355X HBM3E, decimal GB/s
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "shift_kernel_bf16_qwen3-14b-multispan_traffic.json")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_plan(plan, steps: int, warmup: int, stream):
+    import torch
+
+    for _ in range(warmup):
+        plan.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        plan.launch(stream.cuda_stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall, per
+
+
+def spot_check(wl, rows: int = 96, seed: int = 0) -> int:
+    """Compare ``rows`` sampled (layer, token) rows of the output with the oracle."""
+    import numpy as np
+    import torch
+
+    from oracle import kvshift_oracle as orc
+
+    rng = np.random.default_rng(seed)
+    inv = wl.inv_freq.numpy()
+    src_tab = wl.meta["src_table"]
+    dst_slots = wl.dst_index.numpy()
+    spans = wl.spans
+    checked = 0
+    for _ in range(rows):
+        s = int(rng.integers(len(spans)))
+        sp = spans[s]
+        i = int(rng.integers(int(sp["n_tokens"])))
+        layer = int(rng.integers(wl.layers))
+        pos = int(sp["src_pos"]) + i
+        sblk, soff = int(src_tab[pos // 16]), pos % 16
+        slot = int(dst_slots[int(sp["dst_index"]) + i])
+        dblk, doff = slot // 16, slot % 16
+        src_row = wl.src.caches[0][layer][sblk, soff].cpu()  # NHD: [heads, 2D]
+        got = wl.dst.caches[0][layer][dblk, :, doff].cpu()  # HND: [heads, 2D]
+        sb = src_row.view(torch.int16).numpy().view(np.uint16)
+        gb = got.view(torch.int16).numpy().view(np.uint16)
+        want_k = orc.rotate_k_bits(sb[:, :128], int(sp["delta"]), inv, "bf16")
+        if not (np.array_equal(gb[:, :128], want_k) and np.array_equal(gb[:, 128:], sb[:, 128:])):
+            raise AssertionError(f"bench output differs from the oracle at span {s} token {i} layer {layer}")
+        checked += 1
+    return checked
+
+
+def cpu_baseline(reps: int = 3) -> dict:
+    """The reference torch path on the host CPU, config 1 (28 layers x 4,096 tokens)."""
+    import platform
+
+    import torch
+
+    from marathon_amd.workloads import config1_cpu
+    from oracle import torch_path
+
+    cfg = config1_cpu()
+    emb = torch_path.rope_emb_tables(cfg["delta"], cfg["inv_freq"])
+    n = cfg["src"][0].shape[0]
+    layers = len(cfg["src"])
+    best = float("inf")
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        for src, kv in zip(cfg["src"], cfg["kv"]):
+            torch_path.shift_into_paged(src, kv, cfg["slots"], 16, True, emb)
+        dt = time.perf_counter() - t0
+        if i:
+            best = min(best, dt)
+    moved = 2 * sum(s.numel() * s.element_size() for s in cfg["src"])
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        cpu = platform.processor() or cpu
+    return {
+        "value": round(moved / best / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"reference torch shift path (oracle/torch_path.py) on the CPU, Qwen3-0.6B "
+        f"shape: {layers} layers x {n} tokens x 8 heads x 256 bf16, delta +37, flat store -> "
+        f"HND paged cache; best of {reps} after 1 warmup; {best * 1e3:.1f} ms per shift; "
+        f"CPU: {cpu}",
+        "ms_per_shift": round(best * 1e3, 2),
+    }
+
+
+def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
+    """The reference micro-benchmark's shape (scripts/bench_shift_copy.py:24-53)."""
+    import numpy as np
+    import torch
+
+    from marathon_amd.shift_kernels import inv_freq_for
+    from marathon_amd.spans import CacheSet, ShiftPlan, span_array
+
+    n, layers, heads, d, bs = 30720, 40, 8, 128, 16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    blocks = -(-n // bs) + 8
+    src = [torch.randn(n, heads, 2 * d, dtype=torch.bfloat16, device=dev, generator=gen)
+           for _ in range(layers)]
+    kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
+          for _ in range(layers)]
+    table = torch.randperm(blocks, device=dev, generator=gen)
+    pos = torch.arange(n, device=dev)
+    slot = table[pos // bs] * bs + pos % bs
+    plan = ShiftPlan(span_array([(0, 0, 0, 0, n, 186, 0, 0)]), CacheSet([src], "flat"),
+                     CacheSet([kv], "hnd", bs), inv_freq=inv_freq_for(d, 1e6),
+                     src_mode="flat", dst_mode="slots", dst_index=slot)
+    wall, per = time_plan(plan, steps, warmup, stream)
+    ms = float(np.mean(per))
+    out = {
+        "shape": "30,720 tokens x 40 layers x 8 heads x 128, bf16, delta 186, flat store -> "
+        "HND paged (scripts/bench_shift_copy.py)",
+        "ms": round(ms, 4),
+        "GB_s": round(plan.algorithmic_bytes / (ms / 1e3) / 1e9, 1),
+        "reference_rtx5090_ms": 6.54,
+    }
+    del src, kv, plan
+    torch.cuda.empty_cache()
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference-shape", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (for PMC counter scaling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU: the shift needs no collective and this build runs on "
+            "a single MI355X (per-rank sharding is by KV head / layer / session with no "
+            "exchange; see DESIGN.md).  Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    log("building config 3 workload (40 layers, 30,720-token history, 8 spans)")
+    wl = W.config3(dev)
+    plan = wl.plan()
+    torch.cuda.synchronize()
+    log(f"spans={len(wl.spans)} tokens={wl.tokens} bytes={plan.algorithmic_bytes}")
+
+    if args.copy_calibration:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1 GiB device copy done")
+        del a, b
+
+    wall, per = time_plan(plan, args.steps, args.warmup, stream)
+    checked = spot_check(wl)
+    log(f"spot check: {checked} sampled rows bit-identical to the oracle")
+    ms_step = wall / args.steps * 1e3
+    bytes_step = plan.algorithmic_bytes
+    value = bytes_step * args.steps / wall / 1e9
+    ev_ms = float(np.mean(per))
+    achieved = bytes_step / (ev_ms / 1e3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
+
+    extra = {}
+    if not args.no_reference_shape:
+        del wl, plan
+        torch.cuda.empty_cache()
+        log("reference benchmark shape (30,720 x 40, delta 186)")
+        extra["reference_shape"] = reference_shape(dev, max(5, args.steps // 2), args.warmup, stream)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (reference torch path on the host, config 1)")
+        cpu = cpu_baseline()
+
+    tokens = int(bytes_step // (2 * 40 * 8 * 256 * 2))
+    line = {
+        "metric": "fused KV-shift HBM GB/s (% of 8 TB/s peak) and ms per 30k-token shift, 1 GPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: K/V ~ N(0,1) bf16 drawn on device (seed 3), shuffled block tables",
+        "config": {
+            "workload": "qwen3-14b multi-span shift: 40 layers, 8 kv heads, head_dim 128, "
+            "30,720-token history, 8 spans (seed 3), store block layout -> HND paged cache",
+            "tokens_shifted": tokens,
+            "layers": 40,
+            "spans": 8,
+            "bytes_per_step": bytes_step,
+        },
+        "frac_of_peak": round(value / PEAK_GBS, 4),
+        "tokens_per_s": round(tokens / (ms_step / 1e3), 1),
+        "us_per_token": round(ms_step * 1e3 / tokens, 5),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel_ms": round(ev_ms, 4),
+        },
+        "cpu_baseline": cpu,
+        "parity": f"{checked} sampled rows bit-identical to the oracle after timing",
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -18,7 +18,8 @@
  *
  * Conventions shared by every entry point:
  *   - All pointers named "device" are HIP device addresses; nothing is allocated and
- *     nothing is synchronised.  Work is enqueued on `stream` (a hipStream_t; NULL is
+ *     nothing is synchronised (the batched entry point works in a caller-provided
+ *     device workspace).  Work is enqueued on `stream` (a hipStream_t; NULL is
  *     the legacy default stream) and the call returns as soon as it is enqueued.
  *   - Strides are in ELEMENTS of the cache element type.  16-byte alignment of every
  *     base address and of every stride in bytes is required (MKV_ERR_ALIGN otherwise).
@@ -126,17 +127,28 @@ typedef struct mkv_side {
 } mkv_side_t;
 
 /*
- * A batched shift: every span x every layer in ONE launch.
- *   spans     : device [n_spans], 0 <= n_spans <= MKV_MAX_SPANS.
- *   inv_freq  : device fp32 [rotary / 2]; may be NULL when rotary == 0.
- *   k_scale   : device fp32 [layers], fp8 only (NULL otherwise).
- *   error_flags : device int32 [1] or NULL.
+ * A batched shift: every span x every layer, enqueued as two launches (a small plan
+ * kernel that resolves every token's source and destination row and each span's
+ * cos/sin into the workspace, then the shift itself).
+ *   spans        : device [n_spans], 0 <= n_spans <= MKV_MAX_SPANS.
+ *   total_tokens : sum of the spans' n_tokens, known to the caller (it sizes the
+ *                  launch and the workspace); tokens beyond it are not moved and raise
+ *                  MKV_FLAG_SPAN.
+ *   inv_freq     : device fp32 [rotary / 2]; may be NULL when rotary == 0.
+ *   k_scale      : device fp32 [layers], fp8 only (NULL otherwise).
+ *   error_flags  : device int32 [1] or NULL.
+ *   workspace    : device, >= mkv_shift_workspace_size(total_tokens, n_spans, rotary)
+ *                  bytes, 16-byte aligned; overwritten by every call, so calls that
+ *                  overlap on one workspace race.
  */
 typedef struct mkv_shift_desc {
   const mkv_span_t* spans;
   const float* inv_freq;
   const float* k_scale;
   int32_t* error_flags;
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t total_tokens;
   int32_t n_spans;
   int32_t layers;
   int32_t heads;
@@ -158,16 +170,19 @@ typedef struct mkv_shift_desc {
  *             [blocks, heads, bs, 2D] or NHD [blocks, bs, heads, 2D]
  *             (shift_kernels.py:135-138).  kv_num_blocks bounds the slots.
  * slots     : device int64 [n_tokens] flat destination slots (shift_store.py:56-60).
- * inv_freq, rotary, delta : the rotation (rope_shift, shift_kernels.py:68-84);
- *             delta == 0 or rotary == 0 is a plain scatter.  n_tokens == 0 is a no-op.
- * k_scale   : device fp32 [1] for MKV_FP8_E4M3, else NULL.
+ * cos, sgn  : device fp32 [head_size]: the RopeShift tables of one delta
+ *             (shift_kernels.py:50-84: cos[i], and -sin for i < rotary/2, +sin for
+ *             rotary/2 <= i < rotary); cos == NULL is a plain scatter (delta 0).
+ * rotary    : rotated dimensions (2 * len(inv_freq)); dims >= rotary are copied.
+ *             n_tokens == 0 is a no-op.
+ * k_scale   : device fp32 [1] for MKV_FP8_E4M3 when rotating, else NULL.
  */
 int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_head_stride,
                         void* kv, int64_t kv_block_stride, int64_t kv_head_stride,
                         int64_t kv_offset_stride, int64_t kv_num_blocks,
                         const int64_t* slots, int64_t n_tokens, int32_t heads,
                         int32_t head_size, int32_t block_size, int32_t dtype,
-                        const float* inv_freq, int32_t rotary, int32_t delta,
+                        const float* cos, const float* sgn, int32_t rotary,
                         const float* k_scale, int32_t* error_flags, void* stream);
 
 /*
@@ -178,12 +193,15 @@ int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_h
  */
 int mkv_shift_spans(const mkv_shift_desc_t* desc, void* stream);
 
+/* Workspace bytes mkv_shift_spans needs for these sizes (-1 on negative input). */
+int64_t mkv_shift_workspace_size(int64_t total_tokens, int32_t n_spans, int32_t rotary);
+
 /* Human-readable reason for the last non-MKV_OK return on this thread ("" if none). */
 const char* mkv_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. */
 int32_t mkv_abi_version(void);
-#define MKV_ABI_VERSION ((1 << 16) | 0)
+#define MKV_ABI_VERSION ((2 << 16) | 0)
 
 #ifdef __cplusplus
 }

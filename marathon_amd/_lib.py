@@ -42,7 +42,7 @@ MKV_ADDR_TABLE = 2
 
 MKV_MAX_SPANS = 4096
 MKV_MAX_HEAD_SIZE = 512
-MKV_ABI_VERSION = (1 << 16) | 0
+MKV_ABI_VERSION = (2 << 16) | 0
 
 ERROR_NAMES = {
     MKV_ERR_ARG: "MKV_ERR_ARG",
@@ -53,7 +53,13 @@ ERROR_NAMES = {
 }
 
 # Every symbol the header declares; tests check the library exports all of them.
-EXPORTED = ("mkv_scatter_shifted", "mkv_shift_spans", "mkv_last_error", "mkv_abi_version")
+EXPORTED = (
+    "mkv_scatter_shifted",
+    "mkv_shift_spans",
+    "mkv_shift_workspace_size",
+    "mkv_last_error",
+    "mkv_abi_version",
+)
 
 
 class Span(ctypes.Structure):
@@ -108,13 +114,16 @@ class Side(ctypes.Structure):
 
 
 class ShiftDesc(ctypes.Structure):
-    """mkv_shift_desc_t (232 bytes)."""
+    """mkv_shift_desc_t (256 bytes)."""
 
     _fields_ = [
         ("spans", ctypes.c_void_p),
         ("inv_freq", ctypes.c_void_p),
         ("k_scale", ctypes.c_void_p),
         ("error_flags", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+        ("total_tokens", ctypes.c_int64),
         ("n_spans", ctypes.c_int32),
         ("layers", ctypes.c_int32),
         ("heads", ctypes.c_int32),
@@ -126,7 +135,7 @@ class ShiftDesc(ctypes.Structure):
     ]
 
 
-assert ctypes.sizeof(Side) == 88 and ctypes.sizeof(ShiftDesc) == 232
+assert ctypes.sizeof(Side) == 88 and ctypes.sizeof(ShiftDesc) == 256
 
 
 class KVShiftError(RuntimeError):
@@ -145,11 +154,14 @@ def _bind(cdll: ctypes.CDLL) -> ctypes.CDLL:
     i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
     f = cdll.mkv_scatter_shifted
     f.restype = ctypes.c_int
-    f.argtypes = [vp, i64, i64, vp, i64, i64, i64, i64, vp, i64, i32, i32, i32, i32, vp, i32,
+    f.argtypes = [vp, i64, i64, vp, i64, i64, i64, i64, vp, i64, i32, i32, i32, i32, vp, vp,
                   i32, vp, vp, vp]
     f = cdll.mkv_shift_spans
     f.restype = ctypes.c_int
     f.argtypes = [ctypes.POINTER(ShiftDesc), vp]
+    f = cdll.mkv_shift_workspace_size
+    f.restype = ctypes.c_int64
+    f.argtypes = [i64, i32, i32]
     cdll.mkv_last_error.restype = ctypes.c_char_p
     cdll.mkv_last_error.argtypes = []
     cdll.mkv_abi_version.restype = ctypes.c_int32

@@ -9,20 +9,24 @@
 //     write K', V' at dst(s, i), head h        paged: block = slot / bs, off = slot % bs
 //
 // Design (CDNA4, HBM-bound, no MFMA):
-//   * One persistent launch covers every span x every layer.  Work is cut into tiles
-//     of (span, layer, run of tile_tokens tokens); a workgroup walks tiles with a
-//     grid stride.  The per-span tile prefix lives in LDS (built once per workgroup).
+//   * The shift kernel is a one-shot grid over (token tiles) x (layers): a workgroup
+//     moves tile_tokens tokens of one layer and exits.  Measured on MI355X, one-shot
+//     workgroups stream ~25% faster than persistent grid-stride loops, where each
+//     iteration's loads queue behind the previous iteration's stores (gfx9 counts
+//     loads and stores on one vmcnt).
 //   * A row is one (layer, token, head): K[D] then V[D].  Lane j of a row owns the
 //     16-byte chunk j of K and the 16-byte chunk j of V, so each load/store
-//     instruction moves whole, contiguous 16*nK-byte runs (full 128-byte lines).
+//     instruction moves whole, contiguous runs (full 128-byte lines).
+//   * When heads is a multiple of the rows a wave covers, every row of a wave pass
+//     belongs to one token: the token's metadata is read with scalar loads and the
+//     lane address is (uniform base) + (per-lane 32-bit constant).
 //   * rotate_half needs chunk j +- rotary/2: it comes from the partner lane through
 //     ds_bpermute (no second global read of K).
-//   * cos/sin of fl32(delta * inv_freq[f]) are evaluated once per span per workgroup
-//     in double precision, rounded to fp32 and kept in LDS; each lane then holds the
-//     values of its own chunk in registers.
+//   * Batched shifts first run a small plan kernel that resolves every token's source
+//     and destination row (slot arrays / block tables, bounds-checked) into a record,
+//     and evaluates each span's cos/sin once (double precision, rounded to fp32).
+//     Both live in a caller-provided workspace; the library allocates nothing.
 //   * Loads and stores are non-temporal: every byte is touched exactly once.
-//   * Every slot, block id and table index is checked against the capacities given
-//     by the caller; a row that fails is skipped and flagged, never accessed.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -31,17 +35,31 @@
 #include <stdio.h>
 #include <string.h>
 
-#include <mutex>
-
 #include "marathon_kvshift.h"
 
 #pragma clang fp contract(off)
 
+// Tuning knobs (compile-time): non-temporal loads / stores, wave passes per workgroup.
+#ifndef MKV_NT_LOAD
+#define MKV_NT_LOAD 1
+#endif
+#ifndef MKV_NT_STORE
+#define MKV_NT_STORE 1
+#endif
+#ifndef MKV_PASSES_2B
+#define MKV_PASSES_2B 4
+#endif
+#ifndef MKV_PASSES_4B
+#define MKV_PASSES_4B 4
+#endif
+#ifndef MKV_PASSES_1B
+#define MKV_PASSES_1B 2
+#endif
+
 namespace {
 
-constexpr int kThreads = 256;            // 4 waves of 64
+constexpr int kThreads = 256;  // 4 waves of 64
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxHalf = MKV_MAX_HEAD_SIZE / 2;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Global-address-space view: keeps the compiler on global_load/global_store rather
@@ -54,34 +72,41 @@ template <int DT>
 struct Elem;
 template <>
 struct Elem<MKV_BF16> {
-  static constexpr int kBytes = 2, kPerChunk = 8, kUnroll = 4;
+  static constexpr int kBytes = 2, kPerChunk = 8, kPasses = MKV_PASSES_2B;
 };
 template <>
 struct Elem<MKV_F16> {
-  static constexpr int kBytes = 2, kPerChunk = 8, kUnroll = 4;
+  static constexpr int kBytes = 2, kPerChunk = 8, kPasses = MKV_PASSES_2B;
 };
 template <>
 struct Elem<MKV_F32> {
-  static constexpr int kBytes = 4, kPerChunk = 4, kUnroll = 4;
+  static constexpr int kBytes = 4, kPerChunk = 4, kPasses = MKV_PASSES_4B;
 };
 template <>
 struct Elem<MKV_FP8_E4M3> {
-  static constexpr int kBytes = 1, kPerChunk = 16, kUnroll = 2;
+  static constexpr int kBytes = 1, kPerChunk = 16, kPasses = MKV_PASSES_1B;
 };
 
-// -------------------------------------------------------------------- kernel params
+int passes_of(int dt) {
+  switch (dt) {
+    case MKV_FP8_E4M3:
+      return MKV_PASSES_1B;
+    case MKV_F32:
+      return MKV_PASSES_4B;
+    default:
+      return MKV_PASSES_2B;
+  }
+}
 
+// ----------------------------------------------------------------- device structs
+
+// How one side maps a token position to a byte offset inside its buffer.
 struct DevSide {
-  const uint64_t* k_base;  // [groups * layers] (batched) or nullptr (single span)
-  const uint64_t* v_base;
-  uint64_t k_inline;       // single span: K / V base address of the one (group, layer)
-  uint64_t v_inline;
   const void* index;
-  const int64_t* group_slots;  // per-group num_slots, or nullptr
+  const int64_t* group_slots;
   int64_t index_len;
   int64_t num_slots;
   int64_t bstride;  // BYTES
-  int64_t hstride;  // BYTES
   int64_t ostride;  // BYTES
   int64_t block_size;
   int32_t bs_shift;  // log2(block_size), or -1 when block_size is not a power of two
@@ -90,38 +115,105 @@ struct DevSide {
   int32_t pad;
 };
 
-struct KParams {
-  const mkv_span_t* spans;  // batched: device table; single span: nullptr
-  mkv_span_t one;           // single span, passed by value
+// One resolved token of a batched shift (32 bytes), written by plan_kernel.
+struct TokRec {
+  int64_t src_off;  // byte offset of the token's row (head 0, element 0) in its buffer
+  int64_t dst_off;
+  int32_t span;     // -1: nothing to do for this token
+  int32_t delta;
+  int32_t src_base;  // src_group * layers (row of the source base-address tables)
+  int32_t dst_base;
+};
+
+struct PlanParams {
+  const mkv_span_t* spans;
   const float* inv_freq;
-  const float* k_scale;
+  float* tables;  // [n_spans][2][rotary]: cos by element, then sgn by element
+  TokRec* recs;   // [total_tokens]
   int32_t* err;
+  int64_t total_tokens;
   int32_t n_spans;
   int32_t layers;
-  int32_t heads;
-  int32_t head_size;
   int32_t rotary;
-  int32_t tile_tokens;
-  int32_t chunks_per_row;  // nK: 16-byte chunks in K (= lanes per row)
-  int32_t rows_per_wave;
-  uint32_t heads_magic;    // ceil(2^32 / heads): r / heads == umulhi(r, magic) for r < 2^16
   int32_t pad;
   DevSide src;
   DevSide dst;
 };
 
+struct ShiftParams {
+  // single span: bases, the source token stride, slots and the rotation tables
+  const char* s_k;
+  const char* s_v;
+  char* d_k;
+  char* d_v;
+  const int64_t* slots;
+  const float* cos;
+  const float* sgn;
+  int64_t src_tstride;  // BYTES
+  DevSide dst;          // slot -> offset (single span)
+  // batched: records, per-span tables, base-address tables
+  const TokRec* recs;
+  const float* tables;
+  const uint64_t* src_k_base;
+  const uint64_t* src_v_base;
+  const uint64_t* dst_k_base;
+  const uint64_t* dst_v_base;
+  // common
+  const float* k_scale;
+  int32_t* err;
+  int64_t total_tokens;
+  int64_t src_hstride;  // BYTES
+  int64_t dst_hstride;  // BYTES
+  int32_t layers;
+  int32_t heads;
+  int32_t rotary;
+  int32_t tile_tokens;
+  int32_t chunks_per_row;  // nK: 16-byte chunks in K (= lanes per row)
+  int32_t rows_per_wave;
+  uint32_t heads_magic;  // ceil(2^32 / heads): r / heads == umulhi(r, magic), r < 2^16
+  int32_t rotate;        // single span: tables present
+};
+
 // ------------------------------------------------------------------ small helpers
 
+// Read-only metadata through the constant address space: with a uniform address the
+// compiler emits scalar loads (through the scalar cache; nothing is written there).
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 __device__ __forceinline__ u32x4 load16(const char* p) {
+#if MKV_NT_LOAD
   return __builtin_nontemporal_load((const g_u32x4*)p);
+#else
+  return *(const g_u32x4*)p;
+#endif
 }
 __device__ __forceinline__ void store16(char* p, u32x4 v) {
+#if MKV_NT_STORE
   __builtin_nontemporal_store(v, (g_u32x4*)p);
+#else
+  *(g_u32x4*)p = v;
+#endif
 }
 
 __device__ __forceinline__ uint32_t bpermute(int lane_byte_addr, uint32_t v) {
   return static_cast<uint32_t>(
       __builtin_amdgcn_ds_bpermute(lane_byte_addr, static_cast<int>(v)));
+}
+
+template <typename T>
+__device__ __forceinline__ T uniform(T v) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "");
+  if constexpr (sizeof(T) == 4) {
+    return static_cast<T>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+  } else {
+    const uint64_t u = static_cast<uint64_t>(v);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<int>(u & 0xFFFFFFFFu));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32));
+    return static_cast<T>((static_cast<uint64_t>(hi) << 32) | lo);
+  }
 }
 
 // RN(RN(k*c) + RN(kp*s)): the torch path's separate fp32 multiply, multiply, add
@@ -189,14 +281,15 @@ __device__ __forceinline__ float clamp448(float q) {
 }
 
 // Rotate the C elements of one 16-byte chunk.  `mine` is this lane's K chunk,
-// `part` the partner chunk (same element positions, other half of the rotation).
+// `part` the partner chunk (same element positions, other half of the rotation),
+// c / s the cos and signed sin of those positions.
 template <int DT>
 struct Rotor;
 
 template <>
 struct Rotor<MKV_BF16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -213,7 +306,7 @@ struct Rotor<MKV_BF16> {
 template <>
 struct Rotor<MKV_F16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -230,7 +323,7 @@ struct Rotor<MKV_F16> {
 template <>
 struct Rotor<MKV_F32> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -244,7 +337,7 @@ struct Rotor<MKV_F32> {
 template <>
 struct Rotor<MKV_FP8_E4M3> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float scale, float) {
+                                              const float* s, float scale) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -263,11 +356,12 @@ struct Rotor<MKV_FP8_E4M3> {
   }
 };
 
-// Slot of token i of a span on one side; false when any index is out of range.
+// Byte offset of token position `pos0 + i` (index slot `index0 + i`) on one side; false
+// when any index is out of range.  cap / cap_blocks: slots and blocks the buffer holds.
 __device__ __forceinline__ bool resolve(const DevSide& sd, int64_t cap, int64_t cap_blocks,
-                                        int64_t pos0, int64_t index0, int64_t i, int64_t& blk,
-                                        int64_t& off) {
-  int64_t slot;
+                                        int64_t pos0, int64_t index0, int64_t i,
+                                        int64_t& off_bytes) {
+  int64_t blk, off;
   if (sd.mode == MKV_ADDR_TABLE) {
     const int64_t pos = pos0 + i;
     if (pos < 0) return false;
@@ -278,262 +372,332 @@ __device__ __forceinline__ bool resolve(const DevSide& sd, int64_t cap, int64_t 
     if (b < 0 || b >= cap_blocks) return false;
     blk = b;
     off = pos - bi * sd.block_size;
-    return true;
-  }
-  if (sd.mode == MKV_ADDR_SLOTS) {
-    const int64_t ii = index0 + i;
-    if (ii < 0 || ii >= sd.index_len) return false;
-    slot = static_cast<const int64_t*>(sd.index)[ii];
   } else {
-    slot = pos0 + i;
+    int64_t slot;
+    if (sd.mode == MKV_ADDR_SLOTS) {
+      const int64_t ii = index0 + i;
+      if (ii < 0 || ii >= sd.index_len) return false;
+      slot = static_cast<const int64_t*>(sd.index)[ii];
+    } else {
+      slot = pos0 + i;
+    }
+    if (slot < 0 || slot >= cap) return false;
+    if (sd.bs_shift >= 0) {
+      blk = slot >> sd.bs_shift;
+      off = slot & (sd.block_size - 1);
+    } else {
+      blk = slot / sd.block_size;
+      off = slot - blk * sd.block_size;
+    }
   }
-  if (slot < 0 || slot >= cap) return false;
-  if (sd.bs_shift >= 0) {
-    blk = slot >> sd.bs_shift;
-    off = slot & (sd.block_size - 1);
-  } else {
-    blk = slot / sd.block_size;
-    off = slot - blk * sd.block_size;
-  }
+  off_bytes = blk * sd.bstride + off * sd.ostride;
   return true;
 }
 
-__device__ __forceinline__ int64_t span_tiles(const mkv_span_t& sp, const KParams& p) {
-  if (sp.n_tokens <= 0) return 0;
-  if (sp.src_group < 0 || sp.src_group >= p.src.groups) return 0;
-  if (sp.dst_group < 0 || sp.dst_group >= p.dst.groups) return 0;
-  return static_cast<int64_t>(p.layers) *
-         ((static_cast<int64_t>(sp.n_tokens) + p.tile_tokens - 1) / p.tile_tokens);
-}
+// --------------------------------------------------------------------- plan kernel
+//
+// Every workgroup builds the token prefix over spans in LDS, then resolves a
+// grid-stride share of the tokens into records and of (span, frequency) pairs into
+// the cos/sin tables.
 
-__device__ __forceinline__ bool span_bad(const mkv_span_t& sp, const KParams& p) {
-  return sp.n_tokens < 0 || sp.src_group < 0 || sp.src_group >= p.src.groups ||
-         sp.dst_group < 0 || sp.dst_group >= p.dst.groups;
-}
+__global__ __launch_bounds__(kThreads) void plan_kernel(PlanParams p) {
+  extern __shared__ int64_t s_pre[];  // [n_spans + 1]: exclusive prefix of tokens
+  __shared__ int64_t s_part[kThreads];
+  const int tid = threadIdx.x;
+  const int n = p.n_spans;
 
-template <typename T>
-__device__ __forceinline__ T uniform(T v) {
-  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "");
-  if constexpr (sizeof(T) == 4) {
-    return static_cast<T>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
-  } else {
-    const uint64_t u = static_cast<uint64_t>(v);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<int>(u & 0xFFFFFFFFu));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<int>(u >> 32));
-    return static_cast<T>((static_cast<uint64_t>(hi) << 32) | lo);
+  const int per = (n + kThreads - 1) / kThreads;
+  const int b = tid * per;
+  const int e = min(b + per, n);
+  int64_t sum = 0;
+  for (int i = b; i < e; ++i) sum += max(p.spans[i].n_tokens, 0);
+  s_part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kThreads; off <<= 1) {
+    const int64_t v = tid >= off ? s_part[tid - off] : 0;
+    __syncthreads();
+    s_part[tid] += v;
+    __syncthreads();
+  }
+  int64_t run = s_part[tid] - sum;
+  for (int i = b; i < e; ++i) {
+    s_pre[i] = run;
+    run += max(p.spans[i].n_tokens, 0);
+  }
+  if (tid == kThreads - 1) s_pre[n] = s_part[kThreads - 1];
+  __syncthreads();
+  const int64_t actual = s_pre[n];
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kThreads + tid;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kThreads;
+
+  if (gtid == 0 && p.err != nullptr) {
+    bool bad = actual > p.total_tokens;
+    for (int i = 0; i < n; ++i) {
+      const mkv_span_t sp = p.spans[i];
+      bad |= sp.n_tokens < 0 || sp.src_group < 0 || sp.src_group >= p.src.groups ||
+             sp.dst_group < 0 || sp.dst_group >= p.dst.groups;
+    }
+    if (bad) atomicOr(p.err, MKV_FLAG_SPAN);
+  }
+
+  // cos / signed sin per span, element-indexed like the reference's tables
+  const int half = p.rotary / 2;
+  const int64_t pairs = static_cast<int64_t>(n) * half;
+  for (int64_t idx = gtid; idx < pairs; idx += gstride) {
+    const int s = static_cast<int>(idx / half);
+    const int f = static_cast<int>(idx - static_cast<int64_t>(s) * half);
+    const float ang = static_cast<float>(p.spans[s].delta) * p.inv_freq[f];
+    double sd, cd;
+    sincos(static_cast<double>(ang), &sd, &cd);
+    const float c = static_cast<float>(cd);
+    const float sn = static_cast<float>(sd);
+    float* t = p.tables + static_cast<int64_t>(s) * 2 * p.rotary;
+    t[f] = c;
+    t[f + half] = c;
+    t[p.rotary + f] = -sn;
+    t[p.rotary + f + half] = sn;
+  }
+
+  // token records
+  for (int64_t g = gtid; g < p.total_tokens; g += gstride) {
+    TokRec r;
+    r.src_off = 0;
+    r.dst_off = 0;
+    r.span = -1;
+    r.delta = 0;
+    r.src_base = 0;
+    r.dst_base = 0;
+    if (g < actual) {
+      int lo = 0, hi = n;  // largest s with s_pre[s] <= g; then s_pre[s + 1] > g
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_pre[mid] <= g) lo = mid;
+        else hi = mid;
+      }
+      const mkv_span_t sp = p.spans[lo];
+      const bool groups_ok = sp.src_group >= 0 && sp.src_group < p.src.groups &&
+                             sp.dst_group >= 0 && sp.dst_group < p.dst.groups;
+      if (groups_ok) {
+        const int64_t i = g - s_pre[lo];
+        int64_t s_cap = p.src.num_slots, d_cap = p.dst.num_slots;
+        if (p.src.group_slots != nullptr) s_cap = p.src.group_slots[sp.src_group];
+        if (p.dst.group_slots != nullptr) d_cap = p.dst.group_slots[sp.dst_group];
+        int64_t so = 0, dof = 0;
+        const bool s_ok =
+            resolve(p.src, s_cap, s_cap / p.src.block_size, sp.src_pos, sp.src_index, i, so);
+        const bool d_ok =
+            resolve(p.dst, d_cap, d_cap / p.dst.block_size, sp.dst_pos, sp.dst_index, i, dof);
+        if (s_ok && d_ok) {
+          r.src_off = so;
+          r.dst_off = dof;
+          r.span = lo;
+          r.delta = sp.delta;
+          r.src_base = sp.src_group * p.layers;
+          r.dst_base = sp.dst_group * p.layers;
+        } else if (p.err != nullptr) {
+          atomicOr(p.err, (s_ok ? 0 : MKV_FLAG_SRC_RANGE) | (d_ok ? 0 : MKV_FLAG_DST_RANGE));
+        }
+      }
+    }
+    p.recs[g] = r;
   }
 }
 
-// ------------------------------------------------------------------------- kernel
+// -------------------------------------------------------------------- shift kernel
+//
+// Grid (token tiles, layers).  Wave w of the workgroup runs passes q = w + 4u
+// (u < U); pass q covers rows [q * rpw, (q + 1) * rpw) of the tile's token-major
+// (token, head) rows.  UNIFORM: heads % rpw == 0, so a pass is one token.
 
-template <int DT, bool SINGLE>
-__global__ __launch_bounds__(kThreads) void shift_kernel(KParams p) {
+template <int DT, bool BATCHED, bool UNIFORM>
+__global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
   using E = Elem<DT>;
   constexpr int C = E::kPerChunk;
-  constexpr int U = E::kUnroll;
-
-  extern __shared__ int64_t s_prefix[];  // batched: tile prefix [n_spans + 1]
-  __shared__ float s_cos[kMaxHalf];
-  __shared__ float s_sin[kMaxHalf];
-  __shared__ int64_t s_part[kThreads];
+  constexpr int U = E::kPasses;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int nK = p.chunks_per_row;
   const int rpw = p.rows_per_wave;
   const int row_in_wave = lane / nK;
   const int j = lane - row_in_wave * nK;  // chunk index inside K (and inside V)
   const bool lane_live = row_in_wave < rpw;
-  const int wg_rows = rpw * kWaves;
-  const int wg_row = wave * rpw + row_in_wave;
   const int P = p.rotary / (2 * C);  // rotate_half distance, in chunks
   const bool rot_lane = j < 2 * P;
   const int partner = j < P ? lane + P : (rot_lane ? lane - P : lane);
-  const int partner_addr = partner * 4;
-  const int64_t chunk_off = static_cast<int64_t>(j) * 16;
+  const int partner_addr = (partner & 63) * 4;
+  const uint32_t chunk_off = static_cast<uint32_t>(j) * 16u;
   const int H = p.heads;
-  const int half = p.rotary / 2;
+  const int layer = blockIdx.y;
 
-  // ---- tile prefix over spans
-  int64_t total;
-  if constexpr (SINGLE) {
-    total = span_tiles(p.one, p);
-  } else {
-    const int n = p.n_spans;
-    const int per = (n + kThreads - 1) / kThreads;
-    const int b = tid * per;
-    const int e = min(b + per, n);
-    int64_t sum = 0;
-    bool bad = false;
-    for (int i = b; i < e; ++i) {
-      const mkv_span_t sp = p.spans[i];
-      sum += span_tiles(sp, p);
-      bad |= span_bad(sp, p);
-    }
-    if (bad && p.err != nullptr && blockIdx.x == 0) atomicOr(p.err, MKV_FLAG_SPAN);
-    s_part[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < kThreads; off <<= 1) {
-      const int64_t v = tid >= off ? s_part[tid - off] : 0;
-      __syncthreads();
-      s_part[tid] += v;
-      __syncthreads();
-    }
-    int64_t run = s_part[tid] - sum;
-    for (int i = b; i < e; ++i) {
-      s_prefix[i] = run;
-      run += span_tiles(p.spans[i], p);
-    }
-    if (tid == kThreads - 1) s_prefix[n] = s_part[kThreads - 1];
-    __syncthreads();
-    total = s_prefix[n];
-  }
+  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * p.tile_tokens;
+  const int64_t left = p.total_tokens - g0;
+  const int ntok = static_cast<int>(left < p.tile_tokens ? left : p.tile_tokens);
+  const int nrows = ntok * H;
+  // per-lane constant part of the addresses (UNIFORM: lane head = pass head + row_in_wave)
+  const uint32_t s_lane = UNIFORM ? static_cast<uint32_t>(row_in_wave) *
+                                            static_cast<uint32_t>(p.src_hstride) + chunk_off
+                                  : chunk_off;
+  const uint32_t d_lane = UNIFORM ? static_cast<uint32_t>(row_in_wave) *
+                                            static_cast<uint32_t>(p.dst_hstride) + chunk_off
+                                  : chunk_off;
 
-  int cur = -1;
-  mkv_span_t sp = p.one;
-  int64_t sp_t0 = 0, sp_t1 = 0, chunks = 1;
-  bool rotate = false;
+  float scale = 1.0f;
   float cs[C], sg[C];
 #pragma unroll
   for (int e = 0; e < C; ++e) cs[e] = 1.0f, sg[e] = 0.0f;
-
-  for (int64_t tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    if (tile >= sp_t1) {
-      // advance to the span holding this tile (tiles only move forward)
-      int s;
-      if constexpr (SINGLE) {
-        s = 0;
-        sp_t0 = 0;
-        sp_t1 = total;
-      } else {
-        s = cur + 1;
-        while (s_prefix[s + 1] <= tile) ++s;
-        s = uniform(s);
-        sp = p.spans[s];
-        sp_t0 = s_prefix[s];
-        sp_t1 = s_prefix[s + 1];
-      }
-      cur = s;
-      chunks = (static_cast<int64_t>(sp.n_tokens) + p.tile_tokens - 1) / p.tile_tokens;
-      rotate = sp.delta != 0 && p.rotary > 0;
-      if (rotate) {
-        __syncthreads();  // nobody still reads the previous span's table
-        for (int f = tid; f < half; f += kThreads) {
-          const float ang = static_cast<float>(sp.delta) * p.inv_freq[f];
-          double sd, cd;
-          sincos(static_cast<double>(ang), &sd, &cd);
-          s_cos[f] = static_cast<float>(cd);
-          s_sin[f] = static_cast<float>(sd);
-        }
-        __syncthreads();
-        if (rot_lane) {
-          const bool first = j < P;
+  int cur_span = -1;
+  if constexpr (!BATCHED) {
+    if (p.rotate && rot_lane) {
 #pragma unroll
-          for (int e = 0; e < C; ++e) {
-            int f = j * C + e;
-            if (f >= half) f -= half;
-            cs[e] = s_cos[f];
-            sg[e] = first ? -s_sin[f] : s_sin[f];
-          }
-        }
+      for (int e = 0; e < C; ++e) {
+        cs[e] = p.cos[j * C + e];
+        sg[e] = p.sgn[j * C + e];
       }
     }
-
-    // tile counts stay far below 2^31 (a span holds < 2^31 tokens), so 32-bit math
-    const uint32_t local = static_cast<uint32_t>(tile - sp_t0);
-    const uint32_t layer = local / static_cast<uint32_t>(chunks);
-    const int64_t tok0 =
-        static_cast<int64_t>(local - layer * static_cast<uint32_t>(chunks)) * p.tile_tokens;
-    const int ntok = static_cast<int>(min(static_cast<int64_t>(p.tile_tokens),
-                                          static_cast<int64_t>(sp.n_tokens) - tok0));
-    const int nrows = ntok * H;
-
-    const char* sk;
-    const char* sv;
-    char* dk;
-    char* dv;
-    if constexpr (SINGLE) {
-      sk = reinterpret_cast<const char*>(p.src.k_inline);
-      sv = reinterpret_cast<const char*>(p.src.v_inline);
-      dk = reinterpret_cast<char*>(p.dst.k_inline);
-      dv = reinterpret_cast<char*>(p.dst.v_inline);
-    } else {
-      const int64_t si = static_cast<int64_t>(sp.src_group) * p.layers + layer;
-      const int64_t di = static_cast<int64_t>(sp.dst_group) * p.layers + layer;
-      sk = reinterpret_cast<const char*>(p.src.k_base[si]);
-      sv = reinterpret_cast<const char*>(p.src.v_base[si]);
-      dk = reinterpret_cast<char*>(p.dst.k_base[di]);
-      dv = reinterpret_cast<char*>(p.dst.v_base[di]);
-    }
-    if (((reinterpret_cast<uint64_t>(sk) | reinterpret_cast<uint64_t>(sv) |
-          reinterpret_cast<uint64_t>(dk) | reinterpret_cast<uint64_t>(dv)) & 15u) != 0) {
-      if (p.err != nullptr && tid == 0) atomicOr(p.err, MKV_FLAG_ALIGN);
-      continue;  // uniform: the whole workgroup skips this tile
-    }
-    int64_t s_cap = p.src.num_slots, d_cap = p.dst.num_slots;
-    if constexpr (!SINGLE) {
-      if (p.src.group_slots != nullptr) s_cap = p.src.group_slots[sp.src_group];
-      if (p.dst.group_slots != nullptr) d_cap = p.dst.group_slots[sp.dst_group];
-    }
-    // block capacity of a TABLE side, once per tile (block ids are checked against it)
-    const int64_t s_cap_blocks = s_cap / p.src.block_size;
-    const int64_t d_cap_blocks = d_cap / p.dst.block_size;
-    float scale = 1.0f;
     if constexpr (DT == MKV_FP8_E4M3) {
-      if (rotate) scale = p.k_scale[layer];  // k_scale may be NULL when nothing rotates
+      if (p.rotate) scale = ld_const(p.k_scale);
+    }
+  } else {
+    if constexpr (DT == MKV_FP8_E4M3) scale = ld_const(p.k_scale + layer);
+  }
+
+  for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
+    // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
+    // metadata is fetched first, then all base addresses, so the workgroup pays two
+    // metadata round trips in total rather than two per pass.
+    bool live[U];
+    int span_u[U], delta_u[U], head_u[U];
+    int64_t s_at[U], d_at[U];  // byte offsets of the pass's (first) row
+    const char* sbk[U];
+    const char* sbv[U];
+    char* dbk[U];
+    char* dbv[U];
+    int sb_u[U], db_u[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row0 = r0 + (wave + kWaves * u) * rpw;
+      const int r = UNIFORM ? row0 : row0 + row_in_wave;
+      const int rr = r < nrows ? r : nrows - 1;  // clamp: metadata reads stay in range
+      const int t = H == 1 ? rr
+                           : static_cast<int>(__umulhi(static_cast<uint32_t>(rr), p.heads_magic));
+      head_u[u] = rr - t * H;
+      const int64_t g = g0 + t;
+      live[u] = r < nrows;
+      if constexpr (BATCHED) {
+        const TokRec* rp = p.recs + g;
+        span_u[u] = UNIFORM ? ld_const(&rp->span) : rp->span;
+        delta_u[u] = UNIFORM ? ld_const(&rp->delta) : rp->delta;
+        s_at[u] = UNIFORM ? ld_const(&rp->src_off) : rp->src_off;
+        d_at[u] = UNIFORM ? ld_const(&rp->dst_off) : rp->dst_off;
+        sb_u[u] = (UNIFORM ? ld_const(&rp->src_base) : rp->src_base) + layer;
+        db_u[u] = (UNIFORM ? ld_const(&rp->dst_base) : rp->dst_base) + layer;
+      } else {
+        span_u[u] = 0;
+        delta_u[u] = p.rotate;
+        s_at[u] = g * p.src_tstride;
+        const int64_t slot = UNIFORM ? ld_const(p.slots + g) : p.slots[g];
+        if (live[u] && (slot < 0 || slot >= p.dst.num_slots)) {
+          if (p.err != nullptr && (!UNIFORM || lane == 0)) atomicOr(p.err, MKV_FLAG_DST_RANGE);
+          live[u] = false;
+        }
+        int64_t blk, off;
+        if (p.dst.bs_shift >= 0) {
+          blk = slot >> p.dst.bs_shift;
+          off = slot & (p.dst.block_size - 1);
+        } else {
+          blk = slot / p.dst.block_size;
+          off = slot - blk * p.dst.block_size;
+        }
+        d_at[u] = blk * p.dst.bstride + off * p.dst.ostride;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if constexpr (BATCHED) {
+        const int sb = sb_u[u], db = db_u[u];
+        if (UNIFORM && u > 0 && sb == sb_u[0] && db == db_u[0]) {
+          // the usual case: every pass of the tile belongs to one (group, layer)
+          sbk[u] = sbk[0];
+          sbv[u] = sbv[0];
+          dbk[u] = dbk[0];
+          dbv[u] = dbv[0];
+        } else {
+          sbk[u] = reinterpret_cast<const char*>(UNIFORM ? ld_const(p.src_k_base + sb)
+                                                         : p.src_k_base[sb]);
+          sbv[u] = reinterpret_cast<const char*>(UNIFORM ? ld_const(p.src_v_base + sb)
+                                                         : p.src_v_base[sb]);
+          dbk[u] = reinterpret_cast<char*>(UNIFORM ? ld_const(p.dst_k_base + db)
+                                                   : p.dst_k_base[db]);
+          dbv[u] = reinterpret_cast<char*>(UNIFORM ? ld_const(p.dst_v_base + db)
+                                                   : p.dst_v_base[db]);
+        }
+        live[u] = live[u] && span_u[u] >= 0;
+        const bool aligned =
+            ((reinterpret_cast<uint64_t>(sbk[u]) | reinterpret_cast<uint64_t>(sbv[u]) |
+              reinterpret_cast<uint64_t>(dbk[u]) | reinterpret_cast<uint64_t>(dbv[u])) & 15u) == 0;
+        if (live[u] && !aligned) {
+          if (p.err != nullptr && (!UNIFORM || lane == 0)) atomicOr(p.err, MKV_FLAG_ALIGN);
+          live[u] = false;
+        }
+      } else {
+        sbk[u] = p.s_k;
+        sbv[u] = p.s_v;
+        dbk[u] = p.d_k;
+        dbv[u] = p.d_v;
+      }
+      s_at[u] += head_u[u] * p.src_hstride;
+      d_at[u] += head_u[u] * p.dst_hstride;
     }
 
-    for (int r0 = 0; r0 < nrows; r0 += wg_rows * U) {
-      u32x4 kd[U], vd[U];
-      int64_t doff[U];
-      bool ok[U];
+    // ---- phase B: every data load of the workgroup's passes in flight at once
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 kd[U], vd[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int r = r0 + u * wg_rows + wg_row;
-        ok[u] = lane_live && r < nrows;
-        kd[u] = u32x4{0, 0, 0, 0};
-        vd[u] = u32x4{0, 0, 0, 0};
-        doff[u] = 0;
-        if (ok[u]) {
-          const int t = H == 1 ? r
-                               : static_cast<int>(__umulhi(static_cast<uint32_t>(r), p.heads_magic));
-          const int h = r - t * H;
-          const int64_t ti = tok0 + t;
-          int64_t sb, so, db, dof;
-          const bool s_ok =
-              resolve(p.src, s_cap, s_cap_blocks, sp.src_pos, sp.src_index, ti, sb, so);
-          const bool d_ok =
-              resolve(p.dst, d_cap, d_cap_blocks, sp.dst_pos, sp.dst_index, ti, db, dof);
-          if (!(s_ok && d_ok)) {
-            if (p.err != nullptr)
-              atomicOr(p.err, (s_ok ? 0 : MKV_FLAG_SRC_RANGE) | (d_ok ? 0 : MKV_FLAG_DST_RANGE));
-            ok[u] = false;
-          } else {
-            const int64_t soff = sb * p.src.bstride + so * p.src.ostride + h * p.src.hstride + chunk_off;
-            doff[u] = db * p.dst.bstride + dof * p.dst.ostride + h * p.dst.hstride + chunk_off;
-            kd[u] = load16(sk + soff);
-            vd[u] = load16(sv + soff);
+    for (int u = 0; u < U; ++u) {
+      kd[u] = u32x4{0, 0, 0, 0};
+      vd[u] = u32x4{0, 0, 0, 0};
+      if (live[u] && lane_live) {
+        kd[u] = load16(sbk[u] + s_at[u] + s_lane);
+        vd[u] = load16(sbv[u] + s_at[u] + s_lane);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- phase C: rotate K (the whole wave joins the partner exchange)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool wave_rotates = UNIFORM ? (live[u] && delta_u[u] != 0 && p.rotary > 0)
+                                        : (p.rotary > 0);
+      if (!wave_rotates) continue;
+      u32x4 pd;
+      pd[0] = bpermute(partner_addr, kd[u][0]);
+      pd[1] = bpermute(partner_addr, kd[u][1]);
+      pd[2] = bpermute(partner_addr, kd[u][2]);
+      pd[3] = bpermute(partner_addr, kd[u][3]);
+      if (live[u] && lane_live && rot_lane && delta_u[u] != 0) {
+        if constexpr (BATCHED) {
+          if (span_u[u] != cur_span) {
+            const float* tb = p.tables + static_cast<int64_t>(span_u[u]) * 2 * p.rotary;
+#pragma unroll
+            for (int e = 0; e < C; ++e) {
+              cs[e] = tb[j * C + e];
+              sg[e] = tb[p.rotary + j * C + e];
+            }
+            cur_span = span_u[u];
           }
         }
+        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale);
       }
-      if (rotate) {
+    }
+
+    // ---- phase D: stores
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          u32x4 pd;
-          pd[0] = bpermute(partner_addr, kd[u][0]);
-          pd[1] = bpermute(partner_addr, kd[u][1]);
-          pd[2] = bpermute(partner_addr, kd[u][2]);
-          pd[3] = bpermute(partner_addr, kd[u][3]);
-          if (rot_lane) kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale, 0.0f);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (ok[u]) {
-          store16(dk + doff[u], kd[u]);
-          store16(dv + doff[u], vd[u]);
-        }
+    for (int u = 0; u < U; ++u) {
+      if (live[u] && lane_live) {
+        store16(dbk[u] + d_at[u] + d_lane, kd[u]);
+        store16(dbv[u] + d_at[u] + d_lane, vd[u]);
       }
     }
   }
@@ -572,29 +736,12 @@ int ilog2_exact(int64_t v) {
   return s;
 }
 
-struct DevInfo {
-  int cus = 0;
-};
-
-std::mutex g_mu;
-DevInfo g_dev[64];
-
-int device_cus(int dev) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  if (dev < 0 || dev >= 64) return 0;
-  if (g_dev[dev].cus == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      return 0;
-    g_dev[dev].cus = cus;
-  }
-  return g_dev[dev].cus;
-}
-
 bool aligned16(uint64_t v) { return (v & 15u) == 0; }
 
+int64_t align256(int64_t v) { return (v + 255) & ~int64_t{255}; }
+
 // Validate one side's geometry and convert it to the device form.
-int make_side(const mkv_side_t& in, int eb, bool single, DevSide& out, const char* name) {
+int make_side(const mkv_side_t& in, int eb, DevSide& out, int64_t& hstride_b, const char* name) {
   memset(&out, 0, sizeof out);
   if (in.mode != MKV_ADDR_FLAT && in.mode != MKV_ADDR_SLOTS && in.mode != MKV_ADDR_TABLE)
     return fail(MKV_ERR_ARG, "%s: unknown addressing mode %d", name, in.mode);
@@ -602,29 +749,25 @@ int make_side(const mkv_side_t& in, int eb, bool single, DevSide& out, const cha
   if (in.num_slots < 0) return fail(MKV_ERR_ARG, "%s: num_slots < 0", name);
   if (in.mode != MKV_ADDR_FLAT && in.index == nullptr && in.index_len > 0)
     return fail(MKV_ERR_ARG, "%s: index is NULL", name);
-  if (!single && (in.k_base == nullptr || in.v_base == nullptr))
-    return fail(MKV_ERR_ARG, "%s: base-address table is NULL", name);
-  if (!single && in.groups <= 0) return fail(MKV_ERR_ARG, "%s: groups %d", name, in.groups);
-  const int64_t bs = static_cast<int64_t>(in.block_stride) * eb;
-  const int64_t hs = static_cast<int64_t>(in.head_stride) * eb;
-  const int64_t os = static_cast<int64_t>(in.offset_stride) * eb;
+  if (in.groups <= 0) return fail(MKV_ERR_ARG, "%s: groups %d", name, in.groups);
+  const int64_t bs = in.block_stride * eb;
+  const int64_t hs = in.head_stride * eb;
+  const int64_t os = in.offset_stride * eb;
   if (!aligned16(static_cast<uint64_t>(bs)) || !aligned16(static_cast<uint64_t>(hs)) ||
       !aligned16(static_cast<uint64_t>(os)))
     return fail(MKV_ERR_ALIGN, "%s: byte strides (%lld, %lld, %lld) not 16-byte aligned", name,
                 (long long)bs, (long long)hs, (long long)os);
-  out.k_base = in.k_base;
-  out.v_base = in.v_base;
   out.index = in.index;
-  out.group_slots = single ? nullptr : in.group_slots;
+  out.group_slots = in.group_slots;
   out.index_len = in.index == nullptr ? 0 : in.index_len;
   out.num_slots = in.num_slots;
   out.bstride = bs;
-  out.hstride = hs;
   out.ostride = os;
   out.block_size = in.block_size;
   out.bs_shift = ilog2_exact(in.block_size);
   out.mode = in.mode;
-  out.groups = single ? 1 : in.groups;
+  out.groups = in.groups;
+  hstride_b = hs;
   return MKV_OK;
 }
 
@@ -632,15 +775,18 @@ struct Geometry {
   int chunks_per_row;
   int rows_per_wave;
   int tile_tokens;
+  bool uniform;
   uint32_t heads_magic;
 };
 
-int check_geometry(int dtype, int heads, int head_size, int rotary, Geometry& g) {
+int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_hs,
+                   int64_t dst_hs, Geometry& g) {
   const int eb = elem_bytes(dtype);
   if (eb == 0) return fail(MKV_ERR_DTYPE, "unknown dtype %d", dtype);
   if (heads <= 0) return fail(MKV_ERR_ARG, "heads %d", heads);
   if (head_size <= 0 || head_size > MKV_MAX_HEAD_SIZE)
-    return fail(MKV_ERR_UNSUPPORTED, "head_size %d outside (0, %d]", head_size, MKV_MAX_HEAD_SIZE);
+    return fail(MKV_ERR_UNSUPPORTED, "head_size %d outside (0, %d]", head_size,
+                MKV_MAX_HEAD_SIZE);
   if ((head_size * eb) % 16 != 0)
     return fail(MKV_ERR_UNSUPPORTED, "head_size %d x %d bytes is not a multiple of 16 bytes",
                 head_size, eb);
@@ -654,52 +800,59 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, Geometry& g)
   if (g.chunks_per_row > 64)
     return fail(MKV_ERR_UNSUPPORTED, "row of %d chunks exceeds one wave", g.chunks_per_row);
   g.rows_per_wave = 64 / g.chunks_per_row;
-  int unroll = dtype == MKV_FP8_E4M3 ? Elem<MKV_FP8_E4M3>::kUnroll : 4;
-  const int rows = g.rows_per_wave * kWaves * unroll;
+  const int rows = g.rows_per_wave * kWaves * passes_of(dtype);
   g.tile_tokens = rows / heads > 0 ? rows / heads : 1;
-  // the row -> (token, head) split uses a 32-bit reciprocal, exact while
-  // tile_tokens * heads < 2^16 and heads < 2^16
+  // row -> (token, head) uses a 32-bit reciprocal, exact while rows < 2^16
   if (static_cast<int64_t>(g.tile_tokens) * heads >= (1 << 16))
     return fail(MKV_ERR_UNSUPPORTED, "heads %d too large", heads);
   g.heads_magic =
       heads == 1 ? 0u : static_cast<uint32_t>(((uint64_t{1} << 32) + heads - 1) / heads);
+  g.uniform = heads % g.rows_per_wave == 0;
+  // per-lane address parts are 32-bit
+  const int64_t hs_max = src_hs > dst_hs ? src_hs : dst_hs;
+  const int64_t lane_max =
+      (g.rows_per_wave - 1) * hs_max + static_cast<int64_t>(g.chunks_per_row) * 16;
+  if (src_hs < 0 || dst_hs < 0 || lane_max >= (int64_t{1} << 31))
+    return fail(MKV_ERR_UNSUPPORTED, "head strides out of range");
   return MKV_OK;
 }
 
-template <int DT, bool SINGLE>
-int launch_typed(const KParams& kp, int64_t single_tiles, size_t lds, hipStream_t stream) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(MKV_ERR_HIP, "hipGetDevice failed");
-  const int cus = device_cus(dev);
-  if (cus <= 0) return fail(MKV_ERR_HIP, "could not query the CU count of device %d", dev);
-  int per_cu = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      &per_cu, reinterpret_cast<const void*>(&shift_kernel<DT, SINGLE>), kThreads, lds);
-  if (e != hipSuccess || per_cu <= 0) per_cu = 1;
-  int64_t grid = static_cast<int64_t>(cus) * per_cu;
-  if (SINGLE && single_tiles < grid) grid = single_tiles;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL((shift_kernel<DT, SINGLE>), dim3(static_cast<unsigned>(grid)),
-                     dim3(kThreads), lds, stream, kp);
-  e = hipGetLastError();
+template <int DT, bool BATCHED, bool UNIFORM>
+int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t stream) {
+  if (tiles <= 0) return MKV_OK;
+  if (tiles > 0x7FFFFFFF || layers > 65535)
+    return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
+                layers);
+  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM>),
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
+                     dim3(kThreads), 0, stream, sp);
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
   return MKV_OK;
 }
 
-template <bool SINGLE>
-int launch(int dtype, const KParams& kp, int64_t single_tiles, size_t lds, hipStream_t stream) {
+template <bool BATCHED>
+int launch_any(int dtype, bool uniform, const ShiftParams& sp, int64_t tiles, int layers,
+               hipStream_t stream) {
+#define MKV_CASE(DT)                                                             \
+  case DT:                                                                       \
+    return uniform ? launch_shift<DT, BATCHED, true>(sp, tiles, layers, stream)  \
+                   : launch_shift<DT, BATCHED, false>(sp, tiles, layers, stream);
   switch (dtype) {
-    case MKV_BF16:
-      return launch_typed<MKV_BF16, SINGLE>(kp, single_tiles, lds, stream);
-    case MKV_F16:
-      return launch_typed<MKV_F16, SINGLE>(kp, single_tiles, lds, stream);
-    case MKV_F32:
-      return launch_typed<MKV_F32, SINGLE>(kp, single_tiles, lds, stream);
-    case MKV_FP8_E4M3:
-      return launch_typed<MKV_FP8_E4M3, SINGLE>(kp, single_tiles, lds, stream);
+    MKV_CASE(MKV_BF16)
+    MKV_CASE(MKV_F16)
+    MKV_CASE(MKV_F32)
+    MKV_CASE(MKV_FP8_E4M3)
     default:
       return fail(MKV_ERR_DTYPE, "unknown dtype %d", dtype);
   }
+#undef MKV_CASE
+}
+
+int64_t workspace_bytes(int64_t total_tokens, int32_t n_spans, int32_t rotary) {
+  return align256(static_cast<int64_t>(n_spans) * 2 * rotary *
+                  static_cast<int64_t>(sizeof(float))) +
+         total_tokens * static_cast<int64_t>(sizeof(TokRec));
 }
 
 }  // namespace
@@ -710,44 +863,45 @@ extern "C" const char* mkv_last_error(void) { return g_err; }
 
 extern "C" int32_t mkv_abi_version(void) { return MKV_ABI_VERSION; }
 
+extern "C" int64_t mkv_shift_workspace_size(int64_t total_tokens, int32_t n_spans,
+                                            int32_t rotary) {
+  if (total_tokens < 0 || n_spans < 0 || rotary < 0) return -1;
+  return workspace_bytes(total_tokens, n_spans, rotary);
+}
+
 extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
                                    int64_t src_head_stride, void* kv, int64_t kv_block_stride,
                                    int64_t kv_head_stride, int64_t kv_offset_stride,
                                    int64_t kv_num_blocks, const int64_t* slots,
                                    int64_t n_tokens, int32_t heads, int32_t head_size,
-                                   int32_t block_size, int32_t dtype, const float* inv_freq,
-                                   int32_t rotary, int32_t delta, const float* k_scale,
+                                   int32_t block_size, int32_t dtype, const float* cos,
+                                   const float* sgn, int32_t rotary, const float* k_scale,
                                    int32_t* error_flags, void* stream) {
   g_err[0] = '\0';
+  const int eb = elem_bytes(dtype);
+  if (eb == 0) return fail(MKV_ERR_DTYPE, "unknown dtype %d", dtype);
   Geometry g;
-  int rc = check_geometry(dtype, heads, head_size, rotary, g);
+  int rc = check_geometry(dtype, heads, head_size, rotary, src_head_stride * eb,
+                          kv_head_stride * eb, g);
   if (rc != MKV_OK) return rc;
   if (n_tokens < 0) return fail(MKV_ERR_ARG, "n_tokens %lld < 0", (long long)n_tokens);
-  if (n_tokens > INT32_MAX) return fail(MKV_ERR_UNSUPPORTED, "n_tokens exceeds 2^31-1");
   if (n_tokens == 0) return MKV_OK;  // the reference returns early (shift_kernels.py:185)
   if (src == nullptr || kv == nullptr || slots == nullptr)
     return fail(MKV_ERR_ARG, "NULL src, kv or slots");
   if (block_size <= 0) return fail(MKV_ERR_ARG, "block_size %d", block_size);
   if (kv_num_blocks < 0) return fail(MKV_ERR_ARG, "kv_num_blocks < 0");
-  const bool rot = delta != 0 && rotary > 0;
-  if (rot && inv_freq == nullptr) return fail(MKV_ERR_ARG, "inv_freq is NULL");
+  const bool rot = cos != nullptr && rotary > 0;
+  if (cos != nullptr && sgn == nullptr) return fail(MKV_ERR_ARG, "cos without sgn");
   if (dtype == MKV_FP8_E4M3 && rot && k_scale == nullptr)
     return fail(MKV_ERR_ARG, "fp8 needs k_scale");
-  const int eb = elem_bytes(dtype);
   const uint64_t s0 = reinterpret_cast<uint64_t>(src);
   const uint64_t d0 = reinterpret_cast<uint64_t>(kv);
   const uint64_t vofs = static_cast<uint64_t>(head_size) * eb;
   if (!aligned16(s0) || !aligned16(d0))
     return fail(MKV_ERR_ALIGN, "src or kv base address not 16-byte aligned");
+  if (!aligned16(static_cast<uint64_t>(src_token_stride * eb)))
+    return fail(MKV_ERR_ALIGN, "src token stride not 16-byte aligned");
 
-  mkv_side_t s_in{};
-  s_in.index = nullptr;
-  s_in.num_slots = n_tokens;
-  s_in.block_stride = src_token_stride;
-  s_in.head_stride = src_head_stride;
-  s_in.offset_stride = 0;
-  s_in.block_size = 1;
-  s_in.mode = MKV_ADDR_FLAT;
   mkv_side_t d_in{};
   d_in.index = slots;
   d_in.index_len = n_tokens;
@@ -757,76 +911,121 @@ extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
   d_in.offset_stride = kv_offset_stride;
   d_in.block_size = block_size;
   d_in.mode = MKV_ADDR_SLOTS;
+  d_in.groups = 1;
 
-  KParams kp;
-  memset(&kp, 0, sizeof kp);
-  rc = make_side(s_in, eb, true, kp.src, "src");
+  ShiftParams sp;
+  memset(&sp, 0, sizeof sp);
+  int64_t dst_hs = 0;
+  rc = make_side(d_in, eb, sp.dst, dst_hs, "dst");
   if (rc != MKV_OK) return rc;
-  rc = make_side(d_in, eb, true, kp.dst, "dst");
-  if (rc != MKV_OK) return rc;
-  kp.src.k_inline = s0;
-  kp.src.v_inline = s0 + vofs;
-  kp.dst.k_inline = d0;
-  kp.dst.v_inline = d0 + vofs;
-  kp.spans = nullptr;
-  kp.one.src_pos = 0;
-  kp.one.dst_pos = 0;
-  kp.one.src_index = 0;
-  kp.one.dst_index = 0;
-  kp.one.n_tokens = static_cast<int32_t>(n_tokens);
-  kp.one.delta = rot ? delta : 0;
-  kp.one.src_group = 0;
-  kp.one.dst_group = 0;
-  kp.inv_freq = inv_freq;
-  kp.k_scale = k_scale;
-  kp.err = error_flags;
-  kp.n_spans = 1;
-  kp.layers = 1;
-  kp.heads = heads;
-  kp.head_size = head_size;
-  kp.rotary = rot ? rotary : 0;
-  kp.tile_tokens = g.tile_tokens;
-  kp.chunks_per_row = g.chunks_per_row;
-  kp.rows_per_wave = g.rows_per_wave;
-  kp.heads_magic = g.heads_magic;
+  sp.s_k = reinterpret_cast<const char*>(s0);
+  sp.s_v = reinterpret_cast<const char*>(s0 + vofs);
+  sp.d_k = reinterpret_cast<char*>(d0);
+  sp.d_v = reinterpret_cast<char*>(d0 + vofs);
+  sp.slots = slots;
+  sp.cos = cos;
+  sp.sgn = sgn;
+  sp.src_tstride = src_token_stride * eb;
+  sp.k_scale = k_scale;
+  sp.err = error_flags;
+  sp.total_tokens = n_tokens;
+  sp.src_hstride = src_head_stride * eb;
+  sp.dst_hstride = dst_hs;
+  sp.layers = 1;
+  sp.heads = heads;
+  sp.rotary = rot ? rotary : 0;
+  sp.tile_tokens = g.tile_tokens;
+  sp.chunks_per_row = g.chunks_per_row;
+  sp.rows_per_wave = g.rows_per_wave;
+  sp.heads_magic = g.heads_magic;
+  sp.rotate = rot ? 1 : 0;
   const int64_t tiles = (n_tokens + g.tile_tokens - 1) / g.tile_tokens;
-  return launch<true>(dtype, kp, tiles, 0, static_cast<hipStream_t>(stream));
+  return launch_any<false>(dtype, g.uniform, sp, tiles, 1, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
   g_err[0] = '\0';
   if (d == nullptr) return fail(MKV_ERR_ARG, "NULL descriptor");
+  const int eb = elem_bytes(d->dtype);
+  if (eb == 0) return fail(MKV_ERR_DTYPE, "unknown dtype %d", d->dtype);
   Geometry g;
-  int rc = check_geometry(d->dtype, d->heads, d->head_size, d->rotary, g);
+  int rc = check_geometry(d->dtype, d->heads, d->head_size, d->rotary,
+                          d->src.head_stride * eb, d->dst.head_stride * eb, g);
   if (rc != MKV_OK) return rc;
   if (d->n_spans < 0 || d->n_spans > MKV_MAX_SPANS)
     return fail(MKV_ERR_UNSUPPORTED, "n_spans %d outside [0, %d]", d->n_spans, MKV_MAX_SPANS);
-  if (d->n_spans == 0) return MKV_OK;
+  if (d->total_tokens < 0) return fail(MKV_ERR_ARG, "total_tokens < 0");
+  if (d->n_spans == 0 || d->total_tokens == 0) return MKV_OK;
   if (d->spans == nullptr) return fail(MKV_ERR_ARG, "NULL span table");
   if (d->layers <= 0) return fail(MKV_ERR_ARG, "layers %d", d->layers);
   if (d->rotary > 0 && d->inv_freq == nullptr) return fail(MKV_ERR_ARG, "inv_freq is NULL");
-  if (d->dtype == MKV_FP8_E4M3 && d->rotary > 0 && d->k_scale == nullptr)
+  if (d->dtype == MKV_FP8_E4M3 && d->k_scale == nullptr)
     return fail(MKV_ERR_ARG, "fp8 needs k_scale");
-  const int eb = elem_bytes(d->dtype);
-  KParams kp;
-  memset(&kp, 0, sizeof kp);
-  rc = make_side(d->src, eb, false, kp.src, "src");
+  if (d->src.k_base == nullptr || d->src.v_base == nullptr || d->dst.k_base == nullptr ||
+      d->dst.v_base == nullptr)
+    return fail(MKV_ERR_ARG, "NULL base-address table");
+  const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary);
+  if (d->workspace == nullptr || d->workspace_bytes < need)
+    return fail(MKV_ERR_ARG, "workspace of %lld bytes needed (mkv_shift_workspace_size)",
+                (long long)need);
+  if (!aligned16(reinterpret_cast<uint64_t>(d->workspace)))
+    return fail(MKV_ERR_ALIGN, "workspace not 16-byte aligned");
+  const int64_t tiles = (d->total_tokens + g.tile_tokens - 1) / g.tile_tokens;
+  if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "total_tokens too large");
+
+  PlanParams pp;
+  memset(&pp, 0, sizeof pp);
+  int64_t src_hs = 0, dst_hs = 0;
+  rc = make_side(d->src, eb, pp.src, src_hs, "src");
   if (rc != MKV_OK) return rc;
-  rc = make_side(d->dst, eb, false, kp.dst, "dst");
+  rc = make_side(d->dst, eb, pp.dst, dst_hs, "dst");
   if (rc != MKV_OK) return rc;
-  kp.spans = d->spans;
-  kp.inv_freq = d->inv_freq;
-  kp.k_scale = d->k_scale;
-  kp.err = d->error_flags;
-  kp.n_spans = d->n_spans;
-  kp.layers = d->layers;
-  kp.heads = d->heads;
-  kp.head_size = d->head_size;
-  kp.rotary = d->rotary;
-  kp.tile_tokens = g.tile_tokens;
-  kp.chunks_per_row = g.chunks_per_row;
-  kp.rows_per_wave = g.rows_per_wave;
-  kp.heads_magic = g.heads_magic;
+  char* ws = static_cast<char*>(d->workspace);
+  float* tables = reinterpret_cast<float*>(ws);
+  TokRec* recs = reinterpret_cast<TokRec*>(
+      ws + align256(static_cast<int64_t>(d->n_spans) * 2 * d->rotary *
+                    static_cast<int64_t>(sizeof(float))));
+  pp.spans = d->spans;
+  pp.inv_freq = d->inv_freq;
+  pp.tables = tables;
+  pp.recs = recs;
+  pp.err = d->error_flags;
+  pp.total_tokens = d->total_tokens;
+  pp.n_spans = d->n_spans;
+  pp.layers = d->layers;
+  pp.rotary = d->rotary;
+
+  const int64_t pairs = static_cast<int64_t>(d->n_spans) * (d->rotary / 2);
+  const int64_t work = d->total_tokens > pairs ? d->total_tokens : pairs;
+  int64_t plan_grid = (work + kThreads - 1) / kThreads;
+  if (plan_grid > 4096) plan_grid = 4096;
+  if (plan_grid < 1) plan_grid = 1;
   const size_t lds = sizeof(int64_t) * (static_cast<size_t>(d->n_spans) + 1);
-  return launch<false>(d->dtype, kp, 0, lds, static_cast<hipStream_t>(stream));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kThreads), lds,
+                     st, pp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MKV_ERR_HIP, "plan launch failed: %s", hipGetErrorString(e));
+
+  ShiftParams sp;
+  memset(&sp, 0, sizeof sp);
+  sp.recs = recs;
+  sp.tables = tables;
+  sp.src_k_base = d->src.k_base;
+  sp.src_v_base = d->src.v_base;
+  sp.dst_k_base = d->dst.k_base;
+  sp.dst_v_base = d->dst.v_base;
+  sp.k_scale = d->k_scale;
+  sp.err = d->error_flags;
+  sp.total_tokens = d->total_tokens;
+  sp.src_hstride = src_hs;
+  sp.dst_hstride = dst_hs;
+  sp.layers = d->layers;
+  sp.heads = d->heads;
+  sp.rotary = d->rotary;
+  sp.tile_tokens = g.tile_tokens;
+  sp.chunks_per_row = g.chunks_per_row;
+  sp.rows_per_wave = g.rows_per_wave;
+  sp.heads_magic = g.heads_magic;
+  return launch_any<true>(d->dtype, g.uniform, sp, tiles, d->layers, st);
 }

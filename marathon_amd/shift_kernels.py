@@ -3,9 +3,9 @@
 Same names, argument meanings and error behaviour as the reference module:
 
 * :class:`RopeShift` / :func:`rope_shift` -- per-delta rotation tables
-  (shift_kernels.py:50-84).  The tables are kept for callers that read them; the HIP
-  kernel itself only needs ``delta`` and ``inv_freq`` and evaluates cos/sin per span
-  on the device.
+  (shift_kernels.py:50-84), built once per delta on the host and kept on the device;
+  the single-span kernel reads ``cos`` and ``sgn`` as the reference's Triton kernel
+  does (shift_kernels.py:96, :127).
 * :func:`scatter_shifted` -- write ``src`` ``[n, heads, 2*head_size]`` into the paged
   ``kv`` at ``slots``, K re-rotated by delta, V copied bit for bit
   (shift_kernels.py:166-210).  One call is one HIP launch on the current stream.
@@ -180,12 +180,13 @@ def scatter_shifted(
     if slots.numel() != n:
         raise ValueError(f"{slots.numel()} slots for {n} tokens")
     rotate = shift is not None and shift.delta != 0 and shift.rotary > 0
-    inv = None
-    scale = None
+    cos = sgn = scale = None
     if rotate:
-        inv = shift.inv_freq
-        if inv.device != kv.device:
-            inv = inv.to(kv.device)
+        cos, sgn = shift.cos, shift.sgn
+        if cos.device != kv.device:
+            cos, sgn = cos.to(kv.device), sgn.to(kv.device)
+        if cos.numel() != d or sgn.numel() != d:
+            raise ValueError(f"rotation tables of {cos.numel()} for head_size {d}")
         if code == _lib.MKV_FP8_E4M3:
             if k_scale is None:
                 raise ValueError("fp8 KV cache needs k_scale")
@@ -207,9 +208,9 @@ def scatter_shifted(
             d,
             int(block_size),
             code,
-            _ptr(inv),
+            _ptr(cos),
+            _ptr(sgn),
             shift.rotary if rotate else 0,
-            shift.delta if rotate else 0,
             _ptr(scale),
             _ptr(error_flags),
             ctypes.c_void_p(current_stream(kv.device)),

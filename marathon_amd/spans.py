@@ -161,10 +161,22 @@ class ShiftPlan:
 
         self.descs = []
         step = _lib.MKV_MAX_SPANS
-        for lo in range(0, self.n_spans, step):
-            cnt = min(step, self.n_spans - lo)
+        counts = np.maximum(spans["n_tokens"].astype(np.int64), 0) if self.n_spans else None
+        chunks = [(lo, min(step, self.n_spans - lo)) for lo in range(0, self.n_spans, step)]
+        L = _lib.lib()
+        need = max(
+            (L.mkv_shift_workspace_size(int(counts[lo:lo + cnt].sum()), cnt, self.rotary)
+             for lo, cnt in chunks),
+            default=0,
+        )
+        # one workspace serves every chunk: the chunks run in stream order
+        self.workspace = torch.empty(max(int(need), 16), dtype=torch.uint8, device=dev)
+        for lo, cnt in chunks:
             d = _lib.ShiftDesc()
             d.spans = span_bytes.data_ptr() + lo * _lib.SPAN_DTYPE.itemsize
+            d.workspace = self.workspace.data_ptr()
+            d.workspace_bytes = self.workspace.numel()
+            d.total_tokens = int(counts[lo:lo + cnt].sum())
             d.inv_freq = inv_dev.data_ptr() if inv_dev is not None else None
             d.k_scale = scale_dev.data_ptr() if scale_dev is not None else None
             d.error_flags = None
@@ -216,7 +228,8 @@ class ShiftPlan:
         return 2 * self.tokens * self.dst.layers * self.dst.heads * 2 * self.dst.head_size * eb
 
     def launch(self, stream: int | None = None, error_flags: torch.Tensor | None = None) -> None:
-        """Enqueue the shift (one launch per 4096 spans) on ``stream`` (default: current)."""
+        """Enqueue the shift on ``stream`` (default: current): a plan launch and a shift
+        launch per 4096 spans."""
         if stream is None:
             stream = current_stream(self.device)
         L = _lib.lib()

@@ -56,7 +56,9 @@ int main(void) {
   O(mkv_side_t, block_stride); O(mkv_side_t, head_stride); O(mkv_side_t, offset_stride);
   O(mkv_side_t, block_size); O(mkv_side_t, mode); O(mkv_side_t, groups);
   O(mkv_shift_desc_t, spans); O(mkv_shift_desc_t, inv_freq); O(mkv_shift_desc_t, k_scale);
-  O(mkv_shift_desc_t, error_flags); O(mkv_shift_desc_t, n_spans); O(mkv_shift_desc_t, layers);
+  O(mkv_shift_desc_t, error_flags); O(mkv_shift_desc_t, workspace);
+  O(mkv_shift_desc_t, workspace_bytes); O(mkv_shift_desc_t, total_tokens);
+  O(mkv_shift_desc_t, n_spans); O(mkv_shift_desc_t, layers);
   O(mkv_shift_desc_t, heads); O(mkv_shift_desc_t, head_size); O(mkv_shift_desc_t, rotary);
   O(mkv_shift_desc_t, dtype); O(mkv_shift_desc_t, src); O(mkv_shift_desc_t, dst);
   return 0;
@@ -89,7 +91,7 @@ def test_struct_layout_matches_the_header(tmp_path):
 def _scatter(**kw):
     args = dict(src=1 << 20, sts=2048, shs=256, kv=1 << 24, kbs=32768, khs=4096, kos=256,
                 nblk=64, slots=1 << 21, n=8, heads=8, d=128, bs=16, dtype=_lib.MKV_BF16,
-                inv=1 << 22, rot=128, delta=5, scale=None, err=None)
+                cos=1 << 22, sgn=1 << 23, rot=128, scale=None, err=None)
     args.update(kw)
     return _lib.lib().mkv_scatter_shifted(*args.values(), None)
 
@@ -106,7 +108,7 @@ def test_host_side_argument_errors_need_no_gpu():
     assert _scatter(heads=0) == _lib.MKV_ERR_ARG
     assert _scatter(n=-1) == _lib.MKV_ERR_ARG
     assert _scatter(src=None) == _lib.MKV_ERR_ARG
-    assert _scatter(inv=None) == _lib.MKV_ERR_ARG
+    assert _scatter(sgn=None) == _lib.MKV_ERR_ARG  # cos without sgn
     assert _scatter(dtype=_lib.MKV_FP8_E4M3, scale=None) == _lib.MKV_ERR_ARG
     assert _scatter(src=(1 << 20) + 8) == _lib.MKV_ERR_ALIGN
     assert _scatter(sts=2047) == _lib.MKV_ERR_ALIGN
@@ -125,11 +127,22 @@ def test_batched_entry_point_argument_errors_need_no_gpu():
     d.n_spans = _lib.MKV_MAX_SPANS + 1
     assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
     d.n_spans = 1
+    d.total_tokens = 100
     assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG  # NULL spans
     d.spans = 1 << 20
     d.inv_freq = 1 << 21
+    for side in (d.src, d.dst):
+        side.k_base, side.v_base = 1 << 24, 1 << 25
+        side.mode, side.block_size, side.groups = _lib.MKV_ADDR_FLAT, 1, 1
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    assert b"workspace" in lib.mkv_last_error()
+    need = lib.mkv_shift_workspace_size(100, 1, 128)
+    assert need == 2 * 128 * 4 + 100 * 32  # one span's cos/sgn tables + 32 B per token
+    assert lib.mkv_shift_workspace_size(-1, 1, 128) == -1
+    d.workspace, d.workspace_bytes = 1 << 26, need - 1
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    d.workspace_bytes = need
     d.src.mode = 7
-    d.src.block_size = 1
     assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
     assert b"mode" in lib.mkv_last_error()
 
