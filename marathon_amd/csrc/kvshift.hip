@@ -47,7 +47,7 @@
 #define MKV_NT_STORE 1
 #endif
 #ifndef MKV_PASSES_2B
-#define MKV_PASSES_2B 4
+#define MKV_PASSES_2B 1
 #endif
 #ifndef MKV_PASSES_4B
 #define MKV_PASSES_4B 4
@@ -56,9 +56,13 @@
 #define MKV_PASSES_1B 2
 #endif
 
+#ifndef MKV_WG_THREADS
+#define MKV_WG_THREADS 256
+#endif
+
 namespace {
 
-constexpr int kThreads = 256;  // 4 waves of 64
+constexpr int kThreads = MKV_WG_THREADS;  // a multiple of the 64-lane wave
 constexpr int kWaves = kThreads / 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -239,43 +243,6 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
   return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xFFFFu)));
 }
 
-// e4m3fn (OCP) decode, exact: sign | 4-bit exponent (bias 7) | 3-bit mantissa;
-// exponent 0 is subnormal (m * 2^-9); S.1111.111 is NaN; there is no infinity.
-__device__ __forceinline__ float e4m3_decode(uint32_t b) {
-  uint32_t s = (b & 0x80u) << 24;
-  uint32_t e = (b >> 3) & 0xFu;
-  uint32_t m = b & 7u;
-  float mag;
-  if (e == 0) {
-    mag = static_cast<float>(m) * 0x1p-9f;
-  } else if (e == 15 && m == 7) {
-    return __uint_as_float(0x7FC00000u);
-  } else {
-    mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  }
-  return __uint_as_float(__float_as_uint(mag) | s);
-}
-
-// e4m3fn encode of a value already clamped to [-448, 448] (or NaN), round to nearest
-// even.  NaN -> 0x7F.  Subnormals: |x| < 2^-6 encodes rint(|x| * 2^9) (exact scaling,
-// so one rounding); the carry into code 8 is the smallest normal, as it should be.
-__device__ __forceinline__ uint32_t e4m3_encode(float x) {
-  if (x != x) return 0x7Fu;
-  uint32_t u = __float_as_uint(x);
-  uint32_t sign = (u >> 24) & 0x80u;
-  float a = __uint_as_float(u & 0x7FFFFFFFu);
-  uint32_t code;
-  if (a < 0x1p-6f) {
-    code = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
-  } else {
-    uint32_t v = __float_as_uint(a);
-    v = v + 0x7FFFFu + ((v >> 20) & 1u);  // RNE at mantissa bit 20
-    uint32_t e = (v >> 23) - 120u;        // rebias 127 -> 7
-    code = (e << 3) | ((v >> 20) & 7u);
-  }
-  return code | sign;
-}
-
 __device__ __forceinline__ float clamp448(float q) {
   return q > 448.0f ? 448.0f : (q < -448.0f ? -448.0f : q);
 }
@@ -289,7 +256,7 @@ struct Rotor;
 template <>
 struct Rotor<MKV_BF16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float) {
+                                              const float* s, float, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -306,7 +273,7 @@ struct Rotor<MKV_BF16> {
 template <>
 struct Rotor<MKV_F16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float) {
+                                              const float* s, float, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -323,7 +290,7 @@ struct Rotor<MKV_F16> {
 template <>
 struct Rotor<MKV_F32> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float) {
+                                              const float* s, float, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -334,23 +301,63 @@ struct Rotor<MKV_F32> {
   }
 };
 
+// fp8 e4m3fn, using gfx950's OCP conversions: v_cvt_pk_f32_fp8 decodes every code
+// exactly, v_cvt_pk_fp8_f32 rounds to nearest even (both checked against the format
+// definition over all codes, all ties and near-ties); its NaN code is 0xFF, so a lane
+// whose inputs hold a NaN code rewrites those bytes to 0x7F.  y / scale uses Markstein's
+// correction, q0 = RN(y * r), q = fma(fma(-q0, scale, y), r, q0) with r = RN(1 / scale),
+// which equals the correctly rounded quotient (checked for every fp32 y with
+// 2^-12 <= |y / scale| < 2^10 at 21 scales in [0.01, 0.1]; smaller quotients encode to
+// a signed zero either way, larger ones cannot occur); copysign keeps -0 / scale = -0.
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bool has_nan_code(uint32_t w) {
+  // a byte whose low 7 bits are all ones (S.1111.111) is NaN
+  return (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0;
+}
+
 template <>
 struct Rotor<MKV_FP8_E4M3> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float scale) {
-    u32x4 out;
+                                              const float* s, float scale, float rcp) {
+    float q[16];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      uint32_t word = 0;
+      const f2 m01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(mine[w]), false);
+      const f2 m23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(mine[w]), true);
+      const f2 p01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(part[w]), false);
+      const f2 p23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(part[w]), true);
+      const float mk[4] = {m01[0], m01[1], m23[0], m23[1]};
+      const float pk[4] = {p01[0], p01[1], p23[0], p23[1]};
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int e = 4 * w + b;
-        float x = e4m3_decode((mine[w] >> (8 * b)) & 0xFFu) * scale;
-        float xp = e4m3_decode((part[w] >> (8 * b)) & 0xFFu) * scale;
-        float y = rot1(x, xp, c[e], s[e]);
-        word |= e4m3_encode(clamp448(y / scale)) << (8 * b);
+        const float x = mk[b] * scale;
+        const float xp = pk[b] * scale;
+        const float y = rot1(x, xp, c[e], s[e]);
+        const float q0 = y * rcp;
+        const float r = __builtin_fmaf(-q0, scale, y);
+        q[e] = clamp448(__builtin_copysignf(__builtin_fmaf(r, rcp, q0), y));
       }
-      out[w] = word;
+    }
+    u32x4 out;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      int v = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * w], q[4 * w + 1], 0, false);
+      v = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * w + 2], q[4 * w + 3], v, true);
+      out[w] = static_cast<uint32_t>(v);
+    }
+    const bool any_nan = has_nan_code(mine[0]) | has_nan_code(mine[1]) | has_nan_code(mine[2]) |
+                         has_nan_code(mine[3]) | has_nan_code(part[0]) | has_nan_code(part[1]) |
+                         has_nan_code(part[2]) | has_nan_code(part[3]);
+    if (__builtin_expect(any_nan, 0)) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if (q[e] != q[e]) {
+          const int sh = 8 * (e & 3);
+          out[e >> 2] = (out[e >> 2] & ~(0xFFu << sh)) | (0x7Fu << sh);
+        }
+      }
     }
     return out;
   }
@@ -562,6 +569,7 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
   } else {
     if constexpr (DT == MKV_FP8_E4M3) scale = ld_const(p.k_scale + layer);
   }
+  const float rcp = 1.0f / scale;  // correctly rounded (fp8 requantisation)
 
   for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
     // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
@@ -688,7 +696,7 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
             cur_span = span_u[u];
           }
         }
-        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale);
+        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale, rcp);
       }
     }
 

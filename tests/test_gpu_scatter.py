@@ -158,3 +158,52 @@ def test_fp8_single_span(gpu, delta):
     orc.scatter_shifted(bits(src), want, slots.numpy(), 16, True, delta, inv.numpy(), "fp8",
                         k_scale=np.float32(scale))
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("delta", [-1, 7, 1999])
+def test_fp8_every_code_in_k_and_its_partner(gpu, delta):
+    """All 256 e4m3fn codes -- NaN (0x7F, 0xFF), +-0, subnormals, +-448 -- as K elements
+    and as their rotate-half partners, bit-exact against the oracle's rule."""
+    print(f"case fp8 all codes delta={delta}", flush=True)
+    g = torch.Generator().manual_seed(77 + delta)
+    n, heads, d = 64, 8, 128
+    codes = torch.arange(256, dtype=torch.int64)
+    k = codes[torch.randint(0, 256, (n, heads, d), generator=g)]
+    # guarantee every (code, partner code) pairing of a sample set appears
+    k[0, 0, :64] = codes[:64]
+    k[0, 0, 64:] = codes[64:128]
+    k[1, 0, :64] = codes[128:192]
+    k[1, 0, 64:] = codes[192:]
+    v = codes[torch.randint(0, 256, (n, heads, d), generator=g)]
+    src = torch.cat((k, v), -1).to(torch.uint8).view(torch.float8_e4m3fn)
+    kv = torch.zeros(8, heads, 16, 2 * d, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    slots = torch.randperm(128, generator=g)[:n]
+    scale = 0.0625
+    inv = inv_freq()
+    got = bits(_run_gpu(gpu, src, kv, slots, 16, True, rope_shift(delta, d, inv, gpu),
+                        k_scale=scale))
+    want = bits(kv)
+    orc.scatter_shifted(bits(src), want, slots.numpy(), 16, True, delta, inv.numpy(), "fp8",
+                        k_scale=np.float32(scale))
+    assert np.array_equal(got, want), f"{int((got != want).sum())} bytes differ"
+
+
+def test_bf16_special_values(gpu):
+    """NaN, +-inf, +-0, denormals and the largest finite values in K, bit-exact."""
+    print("case bf16 special values", flush=True)
+    g = torch.Generator().manual_seed(5)
+    n, heads, d = 32, 8, 128
+    src = torch.randn(n, heads, 2 * d, generator=g).to(torch.bfloat16)
+    specials = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.0, -0.0, 1e-40, -1e-40,
+                             3.3e38, -3.3e38, 9.2e-41], dtype=torch.float32).to(torch.bfloat16)
+    flat = src.view(-1, 2 * d)
+    idx = torch.randint(0, flat.shape[0], (200,), generator=g)
+    col = torch.randint(0, d, (200,), generator=g)
+    flat[idx, col] = specials[torch.arange(200) % len(specials)]
+    kv = torch.zeros(4, 16, heads, 2 * d, dtype=torch.bfloat16)
+    slots = torch.randperm(64, generator=g)[:n]
+    inv = inv_freq()
+    got = bits(_run_gpu(gpu, src, kv, slots, 16, False, rope_shift(-566, d, inv, gpu)))
+    want = bits(kv)
+    orc.scatter_shifted(bits(src), want, slots.numpy(), 16, False, -566, inv.numpy(), "bf16")
+    assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
