@@ -207,12 +207,14 @@ def main() -> int:
     log(f"spans={len(wl.spans)} tokens={wl.tokens} bytes={plan.algorithmic_bytes}")
 
     if args.copy_calibration:
-        a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        # a plain elementwise kernel of known traffic: reads 1 GiB, writes 1 GiB (a
+        # same-dtype copy_ would go to the DMA engine and show no kernel counters)
+        a = torch.zeros(1 << 28, dtype=torch.float32, device=dev)
         b = torch.empty_like(a)
         for _ in range(3):
-            b.copy_(a)
+            torch.neg(a, out=b)
         torch.cuda.synchronize()
-        log("copy calibration: 3 x 1 GiB device copy done")
+        log("copy calibration: 3 x elementwise 1 GiB -> 1 GiB kernel done")
         del a, b
 
     wall, per = time_plan(plan, args.steps, args.warmup, stream)
