@@ -42,8 +42,10 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
 def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bits, round to nearest even; any NaN -> 0x7FC0.
 
-    Same rule as torch's ``.to(torch.bfloat16)`` on CPU (c10::BFloat16), which is what
-    ``scatter_shifted_torch`` applies to the rotated K (shift_kernels.py:156).
+    The rounding of every non-NaN value is torch's ``.to(torch.bfloat16)``, which is
+    what ``scatter_shifted_torch`` applies to the rotated K (shift_kernels.py:156).  NaN
+    payloads are implementation-defined there (c10's scalar cast gives 0x7FC0, the
+    vectorized CPU cast keeps payload bits); this build canonicalises to 0x7FC0.
     """
     x = np.asarray(x, np.float32)
     u = x.view(np.uint32).astype(np.uint64)

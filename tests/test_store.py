@@ -1,0 +1,253 @@
+"""Host bookkeeping of the shift path on the CPU: slots, the single-writer table, the
+session store and the load/save planners.
+
+Each case restates a case of the reference's tests/test_shift_store.py (cited per test)
+against marathon_amd.shift_store; the store holds CPU tensors here exactly as the
+reference's tests do -- bookkeeping, not KV math.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from marathon_amd.connector import accept_multi, detect_hnd
+from marathon_amd.shift_store import (
+    LoadDecision,
+    SessionTable,
+    ShiftStore,
+    plan_load,
+    plan_save,
+    slots,
+)
+
+
+def _kv(n: int, value: float, heads: int = 2, dim: int = 4) -> torch.Tensor:
+    return torch.full((n, heads, dim), value)
+
+
+def test_slots_map_positions_through_the_block_table():  # :24-27
+    assert slots([7, 3], 2, 6, block_size=4).tolist() == [30, 31, 12, 13]
+
+
+def test_session_table_refuses_a_second_in_flight_writer():  # :33-41
+    t = SessionTable()
+    assert t.acquire("r1", "s")
+    assert not t.acquire("r2", "s")
+    assert t.session_of("r2") is None
+    assert t.conflicts == 1
+    t.release("r1")
+    assert t.acquire("r2", "s")
+    assert t.session_of("r2") == "s"
+
+
+def test_session_table_reacquire_by_the_same_request_is_fine():  # :44-48
+    t = SessionTable()
+    assert t.acquire("r1", "s") and t.acquire("r1", "s")
+    assert t.conflicts == 0
+
+
+def test_session_table_release_of_an_unknown_request_is_a_noop():  # :51-56
+    t = SessionTable()
+    t.acquire("r1", "s")
+    t.release("nobody")
+    assert t.session_of("r1") == "s" and len(t) == 1
+
+
+def test_append_only_saves_extend_the_filled_span():  # :62-67
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    assert st.reserve("a", 0, 100) and st.reserve("a", 100, 50)
+    assert st.covers("a", 0, 150) and not st.covers("a", 0, 151)
+
+
+def test_a_save_that_would_leave_a_hole_is_refused():  # :70-75
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    st.reserve("a", 0, 100)
+    assert not st.reserve("a", 200, 10)
+    assert st.covers("a", 0, 100) and st.refusals == 1
+
+
+def test_an_edit_truncates_everything_above_it():  # :78-84
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    st.reserve("a", 0, 500)
+    assert st.reserve("a", 200, 60)
+    assert st.covers("a", 0, 260) and not st.covers("a", 0, 300)
+
+
+def test_a_span_larger_than_the_budget_is_refused():  # :87-90
+    st = ShiftStore(slab=1024, budget_tokens=1024, device="cpu")
+    assert not st.reserve("a", 0, 2000)
+    assert not st.covers("a", 0, 1)
+
+
+def test_reserve_is_idempotent_so_the_worker_may_call_it_per_layer():  # :93-97
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    for _ in range(5):
+        assert st.reserve("a", 0, 300)
+    assert st.stats()["sessions"] == {"a": 300}
+
+
+def test_write_read_round_trip_and_session_isolation():  # :103-113
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    st.reserve("a", 0, 8)
+    st.reserve("b", 0, 8)
+    st.write("a", "layer0", 0, _kv(8, 1.0))
+    st.write("b", "layer0", 0, _kv(8, 2.0))
+    assert torch.equal(st.read("a", "layer0", 0, 8), _kv(8, 1.0))
+    assert torch.equal(st.read("b", "layer0", 0, 8), _kv(8, 2.0))
+    assert st.read("a", "layer1", 0, 8) is None
+    assert st.read("nobody", "layer0", 0, 8) is None
+
+
+def test_read_past_the_filled_span_returns_none():  # :116-120
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    st.reserve("a", 0, 8)
+    st.write("a", "layer0", 0, _kv(8, 1.0))
+    assert st.read("a", "layer0", 4, 8) is None
+
+
+def test_growth_preserves_already_stored_kv():  # :123-130
+    st = ShiftStore(slab=1024, budget_tokens=8192, device="cpu")
+    st.reserve("a", 0, 100)
+    st.write("a", "layer0", 0, _kv(100, 3.0))
+    st.reserve("a", 100, 2000)
+    st.write("a", "layer0", 100, _kv(2000, 4.0))
+    assert torch.equal(st.read("a", "layer0", 0, 100), _kv(100, 3.0))
+    assert torch.equal(st.read("a", "layer0", 100, 2000), _kv(2000, 4.0))
+
+
+def test_lru_evicts_the_least_recently_used_session():  # :136-145
+    st = ShiftStore(slab=1024, budget_tokens=3072, device="cpu")
+    st.reserve("a", 0, 1000)
+    st.reserve("b", 0, 1000)
+    st.reserve("c", 0, 1000)
+    st.covers("a", 0, 1000)
+    st.reserve("c", 1000, 500)
+    assert st.stats()["evictions"] == 1
+    assert set(st.stats()["sessions"]) == {"a", "c"}
+    assert not st.covers("b", 0, 10)
+
+
+def test_eviction_never_takes_the_session_being_written():  # :148-154
+    st = ShiftStore(slab=1024, budget_tokens=2048, device="cpu")
+    st.reserve("a", 0, 1000)
+    st.reserve("b", 0, 1000)
+    st.reserve("b", 1000, 1000)
+    assert set(st.stats()["sessions"]) == {"b"}
+    assert st.covers("b", 0, 2000)
+
+
+def test_an_evicted_session_is_a_miss_not_a_wrong_load():  # :157-164
+    st = ShiftStore(slab=1024, budget_tokens=2048, device="cpu")
+    st.reserve("a", 0, 1000)
+    st.write("a", "layer0", 0, _kv(1000, 9.0))
+    st.reserve("b", 0, 2000)
+    assert not st.covers("a", 0, 1000)
+    assert st.read("a", "layer0", 0, 1000) is None
+    assert st.misses == 1
+
+
+def test_bookkeeping_only_mode_tracks_positions_without_tensors():  # :167-175
+    sched = ShiftStore(slab=1024, budget_tokens=4096, device="cpu", allocate=False)
+    worker = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    for start, n in ((0, 500), (500, 500), (200, 100)):
+        assert sched.reserve("a", start, n) == worker.reserve("a", start, n)
+    sched.write("a", "layer0", 0, _kv(8, 1.0))
+    assert sched.read("a", "layer0", 0, 8) is None
+    assert sched.stats()["sessions"] == worker.stats()["sessions"] == {"a": 300}
+
+
+def test_stats_reports_tokens_per_session():  # :178-186
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    st.reserve("a", 0, 300)
+    st.reserve("b", 0, 700)
+    st.write("b", "layer0", 0, _kv(700, 1.0))
+    s = st.stats()
+    assert s["sessions"] == {"a": 300, "b": 700}
+    assert s["saved_token_layers"] == 700 and s["budget_tokens"] == 4096
+
+
+def test_the_first_save_may_start_above_zero():  # :189-198
+    st = ShiftStore(slab=1024, budget_tokens=4096, device="cpu")
+    assert st.reserve("a", 16, 600) and st.reserve("a", 616, 600)
+    assert st.covers("a", 616, 600) and st.covers("a", 16, 1200)
+    assert not st.covers("a", 0, 1216)
+    assert st.read("a", "layer0", 0, 16) is None
+
+
+def test_hnd_gather_permute_matches_separated_advanced_indexing():  # :201-218
+    blocks, heads, block_size, dim = 7, 4, 16, 8
+    s = torch.tensor([0, 5, 17, 33, 71, 96, 111], dtype=torch.int64)
+    blk, off = s // block_size, s % block_size
+    hnd = torch.randn(blocks, heads, block_size, dim)
+    assert torch.equal(hnd[blk, :, off], hnd.permute(0, 2, 1, 3)[blk, off])
+    nhd = torch.randn(blocks, block_size, heads, dim)
+    assert nhd[blk, off].shape == (s.numel(), heads, dim)
+
+
+def test_session_cap_pre_sizes_the_first_allocation():  # shift_store.py:114-123
+    st = ShiftStore(slab=1024, budget_tokens=8192, device="cpu", session_cap=4096)
+    st.reserve("a", 0, 10)
+    assert st.used == 4096
+
+
+# ------------------------------------------------------------------- planners
+
+
+def test_plan_load_declines_without_session_or_request():
+    st = ShiftStore(device="cpu", allocate=False)
+    assert plan_load(st, None, {"dst_start": 0, "dst_end": 64, "delta": 0}, 0, 100, 16)[0] is None
+    assert plan_load(st, "s", None, 0, 100, 16)[0] is None
+
+
+def test_plan_load_aligns_to_whole_blocks_and_leaves_a_token():  # shift_store.py:308-312
+    st = ShiftStore(budget_tokens=8192, device="cpu", allocate=False)
+    st.reserve("s", 0, 1000)
+    req = {"dst_start": 32, "dst_end": 500, "delta": -10}
+    d, why = plan_load(st, "s", req, 48, 490, 16)
+    # hi = min(500, (490 - 1) // 16 * 16 = 480) = 480; lo = num_computed = 48
+    assert why == "ok" and d == LoadDecision(48, 480, -10) and d.src_start == 58
+    d, why = plan_load(st, "s", req, 48, 60, 16)  # nothing left after alignment
+    assert d is None and "block alignment" in why
+    d, why = plan_load(st, "s", req, 16, 490, 16)  # local hit stops before dst_start
+    assert d is None and "local hit" in why
+
+
+def test_plan_load_declines_when_the_store_lost_the_source():
+    st = ShiftStore(budget_tokens=8192, device="cpu", allocate=False)
+    st.reserve("s", 0, 100)
+    d, why = plan_load(st, "s", {"dst_start": 0, "dst_end": 400, "delta": 50}, 0, 500, 16)
+    assert d is None and "no longer holds" in why
+
+
+def test_plan_save_full_widens_to_zero_once():  # shift_store.py:327-333
+    st = ShiftStore(budget_tokens=8192, device="cpu", allocate=False)
+    assert plan_save(st, "s", "full", 100, 200) == (0, 200)
+    assert plan_save(st, "s", True, 200, 201) == (200, 201)
+    assert plan_save(st, "s", True, 5, 5) is None
+    assert plan_save(st, None, True, 0, 5) is None
+    assert plan_save(st, "s", False, 0, 5) is None
+
+
+def test_accept_multi_block_aligns_and_drops_what_it_cannot_serve():
+    """vllm_shift_connector.py:225-245."""
+    held = {(32, 96)}
+
+    def covers(start, n):
+        return any(a <= start and start + n <= b for a, b in held)
+
+    loads = [
+        {"dst_start": 40, "dst_end": 120, "delta": -8},  # -> [48, 112) src [56, 120): lost
+        {"dst_start": 17, "dst_end": 90, "delta": -5},  # -> [32, 80) src [37, 85): held
+        {"dst_start": 100, "dst_end": 110, "delta": 0},  # < one block after alignment
+    ]
+    got = accept_multi(loads, num_computed=20, num_prompt_tokens=200, block_size=16, covers=covers)
+    assert got == [{"dst_start": 32, "dst_end": 80, "delta": -5}]
+
+
+@pytest.mark.parametrize(
+    "shape,hnd",
+    [((10, 8, 16, 256), True), ((10, 16, 8, 256), False), ((10, 16, 16, 256), False)],
+)
+def test_layout_detection(shape, hnd):  # vllm_shift_connector.py:396-402
+    assert detect_hnd(shape, 16) is hnd
