@@ -29,6 +29,16 @@ logger = logging.getLogger("marathon_amd.shift")
 
 
 @dataclass
+class Save:
+    """One save of a step (vllm_shift_connector.py:143-151): the positions this step
+    computed, ``slots`` in the paged cache, stored from ``dst_start``."""
+
+    session: str
+    slots: torch.Tensor  # int64 [T]
+    dst_start: int
+
+
+@dataclass
 class Load:
     """One load of a step (vllm_shift_connector.py:135-140)."""
 
@@ -176,3 +186,70 @@ class ShiftLoader:
                 plan.algorithmic_bytes / 1e9 / max(ms / 1e3, 1e-12),
             )
         return offset * len(names)
+
+
+class ShiftSaver:
+    """Save path: paged cache -> session store, gathered on the device.
+
+    The reference's ``save_kv_layer`` (vllm_shift_connector.py:539-553) reserves the
+    span, gathers ``[T, heads, 2D]`` with advanced indexing (``_gather``, :418-442) and
+    copies it into the store buffer (``ShiftStore.write``, shift_store.py:225-236).
+    Here the gather kernel reads the paged rows and writes them straight into each
+    session's buffer (delta 0: a pure copy), one launch for every save of the call.
+    """
+
+    def __init__(self, store: ShiftStore, block_size: int):
+        self.store = store
+        self.block_size = int(block_size)
+        self.last_plan: ShiftPlan | None = None
+
+    def _plan(self, names: list, caches: list, saves: list) -> int:
+        first = caches[0]
+        hnd = detect_hnd(first.shape, self.block_size)
+        row_shape = (first.shape[1] if hnd else first.shape[2], first.shape[3])
+        groups: dict[str, int] = {}
+        bufs: list[list] = []
+        rows, slot_parts, offset = [], [], 0
+        for save in saves:
+            n = int(save.slots.numel())
+            if n == 0:
+                continue
+            # mirrors the scheduler's reserve for this step; idempotent across layers
+            if not self.store.reserve(save.session, save.dst_start, n):
+                continue
+            targets = [self.store.write_target(save.session, name, save.dst_start, n, row_shape,
+                                               first.dtype, first.device) for name in names]
+            if any(t is None for t in targets):
+                continue
+            g = groups.get(save.session)
+            if g is None:
+                g = groups[save.session] = len(bufs)
+                bufs.append(targets)
+            else:
+                bufs[g] = targets  # a save may have grown (reallocated) the buffers
+            rows.append((0, int(save.dst_start), offset, 0, n, 0, 0, g))
+            slot_parts.append(save.slots.to(torch.int64).reshape(-1))
+            offset += n
+        if not rows:
+            return 0
+        plan = ShiftPlan(
+            np.array(rows, dtype=_lib.SPAN_DTYPE),
+            CacheSet([caches], "hnd" if hnd else "nhd", self.block_size),
+            CacheSet(bufs, "flat"),
+            inv_freq=None,
+            src_mode="slots",
+            src_index=torch.cat(slot_parts),
+            dst_mode="flat",
+        )
+        plan.launch()
+        self.last_plan = plan
+        return offset * len(names)
+
+    def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, saves: list) -> int:
+        """One layer, every save of the step (the reference's per-layer hook)."""
+        return self._plan([layer_name], [kv_layer], saves)
+
+    def save_all(self, kv_caches: dict, saves: list) -> int:
+        """Every layer and every save of the step in one launch (at the end of a step)."""
+        names = list(kv_caches)
+        return self._plan(names, [kv_caches[n] for n in names], saves)

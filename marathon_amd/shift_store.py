@@ -197,6 +197,26 @@ class ShiftStore:
         entry = self._sessions.get(session)
         return None if entry is None else entry.layers.get(layer)
 
+    def write_target(
+        self, session: str, layer: str, dst_start: int, n: int, row_shape, dtype, device
+    ) -> torch.Tensor | None:
+        """The buffer a device-side save of ``[dst_start, dst_start + n)`` writes into.
+
+        Same preconditions and accounting as :meth:`write` (shift_store.py:225-236):
+        None when the session is unknown, the span exceeds the capacity or the store is
+        the tensor-free mirror; the layer's buffer is allocated on first use.  The caller
+        fills the rows (the save kernel gathers them straight out of the paged cache).
+        """
+        entry = self._sessions.get(session)
+        if entry is None or dst_start + n > entry.capacity or not self.allocate:
+            return None
+        buf = entry.layers.get(layer)
+        if buf is None:
+            buf = torch.zeros((entry.capacity, *row_shape), dtype=dtype, device=device)
+            entry.layers[layer] = buf
+        self.saved_token_layers += n
+        return buf
+
     def drop(self, session: str) -> None:
         self._sessions.pop(session, None)
 

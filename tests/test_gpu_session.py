@@ -1,0 +1,217 @@
+"""End-to-end paged sessions on the GPU: the real store, planners, loader and saver.
+
+The reference's CPU harness (tests/test_paged_depth.py:53-180, FingerprintEngine) models
+KV as the token id, which proves placement but never values.  Here every token's KV is
+real: K at position p is RoPE(table_k[token], p) (bf16), V is table_v[token].  A
+session of front-of-view edits -- the oldest message demoted to a stub every turn, so
+every turn shifts the rest of the history left -- runs through plan_load, the HIP
+loader (re-rotation), a prefill of what is left, and per-step saves through the HIP
+saver (paged -> store).  After every request every position of every layer is checked:
+V bit-exact, K within the rounding that its history of shifts allows.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from marathon_amd import ShiftStore, plan_load, plan_save, slots
+from marathon_amd.connector import Load, Save, ShiftLoader, ShiftSaver
+from marathon_amd.shift_kernels import inv_freq_for
+
+pytestmark = pytest.mark.gpu
+
+H, D, BS, LAYERS = 8, 128, 16, 4
+FILLER = "deterministic filler that makes a message worth several blocks of tokens "
+
+
+class RealKVEngine:
+    """A paged KV cache with block-level prefix caching, driven by the real decisions."""
+
+    def __init__(self, dev, blocks=1024, seed=0):
+        self.dev = dev
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.table_k = torch.randn(256, H, D, dtype=torch.float64, device=dev, generator=g)
+        self.table_v = torch.randn(256, H, D, device=dev, generator=g).to(torch.bfloat16)
+        self.inv = inv_freq_for(D, 1e6)
+        self.inv64 = self.inv.to(dev, torch.float64)
+        self.kv = {f"layer{i}": torch.zeros(blocks, H, BS, 2 * D, dtype=torch.bfloat16, device=dev)
+                   for i in range(LAYERS)}
+        self.store = ShiftStore(budget_tokens=1 << 16, device=str(dev), slab=1024)
+        self.loader = ShiftLoader(self.store, BS, self.inv)
+        self.loader.register_kv_caches(self.kv)
+        self.saver = ShiftSaver(self.store, BS)
+        self.next_block = 0
+        self.prefix: dict[tuple, int] = {}
+        self.shifts = torch.zeros(blocks * BS, dtype=torch.int32)  # per slot: re-rotations
+        self.store_shifts: dict[str, torch.Tensor] = {}
+        self.loads = 0
+        self.declines: list[str] = []
+
+    # -- model: fresh KV of tokens at positions
+    def fresh(self, ids: torch.Tensor, pos: torch.Tensor):
+        ang = pos.to(self.dev, torch.float64)[:, None] * self.inv64[None, :]
+        emb = torch.cat((ang, ang), -1)[:, None, :]
+        base = self.table_k[ids.to(self.dev)]
+        rot = torch.cat((-base[..., D // 2:], base[..., : D // 2]), -1)
+        return base * emb.cos() + rot * emb.sin(), self.table_v[ids.to(self.dev)]
+
+    def _write_fresh(self, blocks, ids, lo, hi):
+        if hi <= lo:
+            return
+        sl = slots(blocks, lo, hi, BS)
+        k, v = self.fresh(torch.tensor(ids[lo:hi]), torch.arange(lo, hi))
+        row = torch.cat((k.to(torch.bfloat16), v), -1)
+        s = sl.to(self.dev)
+        for cache in self.kv.values():
+            cache[s // BS, :, s % BS] = row
+        self.shifts[sl] = 0
+
+    def _blocks_for(self, ids):
+        blocks, hit, broken = [], 0, False
+        for k in range(-(-len(ids) // BS)):
+            key = tuple(ids[: (k + 1) * BS])
+            cached = None if broken else self.prefix.get(key)
+            if cached is not None and (k + 1) * BS <= len(ids):
+                blocks.append(cached)
+                hit = (k + 1) * BS
+            else:
+                broken = True
+                blocks.append(self.next_block)
+                self.next_block += 1
+        return blocks, hit
+
+    def _verify(self, blocks, ids):
+        n = len(ids)
+        sl = slots(blocks, 0, n, BS)
+        k_want, v_want = self.fresh(torch.tensor(ids), torch.arange(n))
+        s = sl.to(self.dev)
+        nshift = self.shifts[sl].to(self.dev, torch.float64)[:, None, None]
+        m = torch.maximum(k_want.abs(), torch.roll(k_want, D // 2, -1).abs())
+        bound = 2.0**-8 * (2 + 2 * nshift) * m + 1e-6
+        for name, cache in self.kv.items():
+            got = cache[s // BS, :, s % BS]
+            assert torch.equal(got[..., D:], v_want), f"{name}: V differs"
+            err = (got[..., :D].to(torch.float64) - k_want).abs()
+            assert bool((err <= bound).all()), f"{name}: K beyond its rounding bound"
+
+    def _save(self, params, blocks, lo, hi, session):
+        window = plan_save(self.store, session, params.get("save"), lo, hi)
+        if window is None:
+            return
+        if params.get("save") == "full":
+            params["save"] = True
+        lo, hi = window
+        sl = slots(blocks, lo, hi, BS)
+        self.saver.save_all(self.kv, [Save(session, sl, lo)])
+        st = self.store_shifts.setdefault(session, torch.zeros(1 << 16, dtype=torch.int32))
+        st[lo:hi] = self.shifts[sl]
+
+    def generate(self, ids, session, max_tokens, load=None, save=False):
+        blocks, num_computed = self._blocks_for(ids)
+        params = {"save": save}
+        decision, why = plan_load(self.store, session, load, num_computed, len(ids), BS)
+        if load and decision is None:
+            self.declines.append(why)
+        if decision is not None:
+            sl = slots(blocks, decision.lo, decision.hi, BS)
+            self.loader.start_load_kv([Load(session, sl, decision.src_start, decision.delta)])
+            st = self.store_shifts[session]
+            self.shifts[sl] = st[decision.src_start:decision.src_start + len(sl)] + int(
+                decision.delta != 0)
+            num_computed = decision.hi
+            self.loads += 1
+        self._write_fresh(blocks, ids, num_computed, len(ids))
+        torch.cuda.synchronize(self.dev)
+        self._verify(blocks, ids)
+        self._save(params, blocks, num_computed, len(ids), session)
+        cur_ids = list(ids)
+        for _ in range(max_tokens):
+            cur = len(cur_ids)
+            if cur // BS >= len(blocks):
+                blocks.append(self.next_block)
+                self.next_block += 1
+            cur_ids.append(1)
+            self._write_fresh(blocks, cur_ids, cur, cur + 1)
+            self._save(params, blocks, cur, cur + 1, session)
+        for k in range(len(ids) // BS):
+            self.prefix.setdefault(tuple(ids[: (k + 1) * BS]), blocks[k])
+        torch.cuda.synchronize(self.dev)
+
+
+def _prompt(messages):
+    pieces = [list(f"{m['role']}: {m['content']}\n".encode()) for m in messages]
+    return [i for p in pieces for i in p] + [10], pieces
+
+
+def _phases(load, n_prompt):
+    """The reference's phases() for one segment (reuse_plan.py:312-342)."""
+    lo = -(-load["dst_start"] // BS) * BS
+    hi = load["dst_end"] // BS * BS
+    if not (hi - lo >= BS and lo > 0 and hi < n_prompt):
+        return []
+    return [(lo, None), (n_prompt, {"dst_start": lo, "dst_end": hi, "delta": load["delta"]})]
+
+
+def test_front_edits_through_the_real_kernels(gpu):
+    eng = RealKVEngine(gpu)
+    messages, keep_last, turns = [], 3, 9
+    prompt_pieces = None  # pieces of the previous request's prompt: what the store holds
+    for t in range(turns):
+        print(f"case session turn {t}", flush=True)
+        load = None
+        if t >= keep_last:
+            d = t - keep_last
+            i = 2 * d  # the oldest live user message (user/assistant alternate)
+            old_pieces = prompt_pieces
+            messages[i] = {"role": "user", "content": f"[cold #{d} {d:08x}]"}
+            new_pieces = _prompt(messages)[1]
+            # reused: the messages after the edited one that the previous prompt held
+            # (the assistant reply appended since then was never in the store)
+            old_start = sum(len(p) for p in old_pieces[: i + 1])
+            new_start = sum(len(p) for p in new_pieces[: i + 1])
+            end = new_start + sum(len(p) for p in old_pieces[i + 1:])
+            load = {"dst_start": new_start, "dst_end": end, "delta": new_start - old_start}
+        messages.append({"role": "user", "content": f"Turn {t}. {FILLER * 3}"})
+        ids, pieces = _prompt(messages)
+        prompt_pieces = pieces
+        phases = _phases(load, len(ids)) if load else []
+        if phases:
+            for length, ld in phases[:-1]:
+                eng.generate(ids[:length], "s", 1, load=ld)
+            eng.generate(ids, "s", 3, load=phases[-1][1], save="full")
+        else:
+            eng.generate(ids, "s", 3, save="full" if t else True)
+        messages.append({"role": "assistant", "content": f"ok {t}"})
+    assert eng.loads >= turns - keep_last - 1, (eng.loads, eng.declines)
+    assert int(eng.shifts.max()) >= 2  # some KV was re-rotated more than once
+
+
+def test_saver_matches_a_torch_gather(gpu):
+    """save_all / save_kv_layer land exactly the paged rows (both layouts)."""
+    for hnd in (True, False):
+        print(f"case saver hnd={hnd}", flush=True)
+        g = torch.Generator(device=gpu)
+        g.manual_seed(int(hnd))
+        shape = (64, H, BS, 2 * D) if hnd else (64, BS, H, 2 * D)
+        kv = {f"l{i}": torch.randn(shape, device=gpu, generator=g).to(torch.bfloat16)
+              for i in range(3)}
+        store = ShiftStore(budget_tokens=8192, device=str(gpu), slab=512)
+        saver = ShiftSaver(store, BS)
+        perm = torch.randperm(64).tolist()
+        sa = Save("a", slots(perm[:20], 5, 5 + 300, BS), 0)
+        sb = Save("b", slots(perm[20:], 16, 16 + 200, BS), 16)
+        assert store.reserve("b", 0, 16)  # "b" holds [0, 16) already
+        n = saver.save_all(kv, [sa, sb])
+        assert n == 500 * 3
+        layer_rows = saver.save_kv_layer("l0", kv["l0"], [Save("a", slots(perm[:20], 5, 5 + 300, BS), 0)])
+        assert layer_rows == 300
+        torch.cuda.synchronize(gpu)
+        for name, cache in kv.items():
+            src = cache.permute(0, 2, 1, 3) if hnd else cache
+            for sv in (sa, sb):
+                s = sv.slots.to(gpu)
+                want = src[s // BS, s % BS]
+                got = store.read(sv.session, name, sv.dst_start, s.numel())
+                assert torch.equal(got, want), (hnd, name, sv.session)
