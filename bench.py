@@ -173,13 +173,44 @@ def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def other_configs(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: the other GPU configurations, one launch per step each."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+
+    out = {}
+    for name, make in (("config2_qwen3_8b_single_span_bf16", lambda: W.config2(dev)),
+                       ("config4_qwen3_14b_multispan_fp8", lambda: W.config4(dev)),
+                       ("config5_32_sessions_batched_bf16", lambda: W.config5(dev))):
+        log(f"timing {name}")
+        wl = make()
+        plan = wl.plan()
+        _, per = time_plan(plan, steps, warmup, stream)
+        ms = float(np.mean(per))
+        out[name] = {
+            "tokens": wl.tokens,
+            "layers": wl.layers,
+            "spans": int(len(wl.spans)),
+            "ms": round(ms, 4),
+            "GB_s": round(plan.algorithmic_bytes / (ms / 1e3) / 1e9, 1),
+            "frac_of_peak": round(plan.algorithmic_bytes / (ms / 1e3) / 1e9 / PEAK_GBS, 4),
+        }
+        del wl, plan
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-shape", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the informational timings of configs 2, 4 and 5")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (for PMC counter scaling)")
     args = ap.parse_args()
@@ -236,6 +267,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("reference benchmark shape (30,720 x 40, delta 186)")
         extra["reference_shape"] = reference_shape(dev, max(5, args.steps // 2), args.warmup, stream)
+    if not args.no_other_configs:
+        extra["other_configs"] = other_configs(dev, max(5, args.steps // 2), args.warmup, stream)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (reference torch path on the host, config 1)")

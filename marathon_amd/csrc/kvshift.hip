@@ -53,7 +53,7 @@
 #define MKV_PASSES_4B 4
 #endif
 #ifndef MKV_PASSES_1B
-#define MKV_PASSES_1B 2
+#define MKV_PASSES_1B 4
 #endif
 
 #ifndef MKV_WG_THREADS
