@@ -59,6 +59,12 @@
 #ifndef MKV_WG_THREADS
 #define MKV_WG_THREADS 256
 #endif
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs; with
+// the remap, XCD k walks the k-th contiguous eighth of the tiles (smaller per-XCD set
+// of pages in flight).  0 = plain order.
+#ifndef MKV_XCDS
+#define MKV_XCDS 8
+#endif
 
 namespace {
 
@@ -538,8 +544,15 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
   const int H = p.heads;
   const int layer = blockIdx.y;
 
-  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * p.tile_tokens;
+  int64_t tile = blockIdx.x;
+  if (MKV_XCDS > 1) {
+    // gridDim.x is a multiple of MKV_XCDS; the map is a bijection on [0, gridDim.x)
+    const int64_t per = gridDim.x / MKV_XCDS;
+    tile = (blockIdx.x % MKV_XCDS) * per + blockIdx.x / MKV_XCDS;
+  }
+  const int64_t g0 = tile * p.tile_tokens;
   const int64_t left = p.total_tokens - g0;
+  if (left <= 0) return;  // padding workgroups of the XCD-aware grid
   const int ntok = static_cast<int>(left < p.tile_tokens ? left : p.tile_tokens);
   const int nrows = ntok * H;
   // per-lane constant part of the addresses (UNIFORM: lane head = pass head + row_in_wave)
@@ -827,7 +840,9 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_
 
 template <int DT, bool BATCHED, bool UNIFORM>
 int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t stream) {
+  // tiles is rounded up to a multiple of MKV_XCDS below; extra workgroups exit at once
   if (tiles <= 0) return MKV_OK;
+  if (MKV_XCDS > 1) tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
   if (tiles > 0x7FFFFFFF || layers > 65535)
     return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
                 layers);
