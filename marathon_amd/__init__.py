@@ -2,12 +2,14 @@
 
 Host API (mirrors src/marathon/shift_kernels.py and src/marathon/shift_store.py):
 ``rope_shift``, ``RopeShift``, ``scatter_shifted``, ``use_hip``, ``warmup``,
-``ShiftStore``, ``SessionTable``, ``slots``, ``plan_load``, ``plan_save``; batched
+``ShiftStore``, ``SessionTable``, ``slots``, ``plan_load``, ``plan_save``; the
+block-layout :class:`BlockShiftStore` (preallocated pool, per-position validity); batched
 launches through :class:`marathon_amd.spans.ShiftPlan`; the worker-side load path in
 :mod:`marathon_amd.connector`.  Everything that touches KV runs in hand-written gfx950
 kernels (``csrc/kvshift.hip``) behind the C ABI in ``include/marathon_kvshift.h``.
 """
 
+from .block_store import BlockShiftStore
 from .shift_kernels import RopeShift, inv_freq_for, rope_shift, scatter_shifted, use_hip, warmup
 from .shift_store import (
     DEFAULT_STORE_TOKENS,
@@ -32,6 +34,7 @@ __all__ = [
     "LoadDecision",
     "SessionTable",
     "ShiftStore",
+    "BlockShiftStore",
     "plan_load",
     "plan_save",
     "slots",

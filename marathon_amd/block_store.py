@@ -1,0 +1,299 @@
+"""Block-layout session store: fixed 16-token blocks of one preallocated pool per layer.
+
+The reference's ``ShiftStore`` (src/marathon/shift_store.py:101-266) keeps each session
+in a flat ``[capacity, heads, 2D]`` buffer per layer.  It grows by geometric realloc plus
+a copy of everything already stored (``_grow``, :149-175), and it has one validity window
+``[base, filled)``: a save at or below ``filled`` truncates everything above it.  That
+window is why the generation-0 address book (src/marathon/remap.py) cannot be wired:
+under no-resave, the gaps between reused spans are saved at lower indices, and each such
+save destroys the bytes the remap addresses higher up (docs/single-request-load.md,
+"Design 2"; src/marathon/server.py:267-276 raises for it).
+
+:class:`BlockShiftStore` keeps the reference's API (``reserve`` / ``covers`` / ``write``
+/ ``read`` / ``drop`` / ``stats``, the same return values and counters) over a different
+memory layout:
+
+* **Pool.** Per layer, one device tensor ``[pool_blocks, block_size, heads, 2D]``,
+  allocated once on the layer's first save.  This is NHD block layout: the
+  ``MKV_ADDR_TABLE`` source and destination layout of the HIP kernels.  A session owns a
+  block table: logical block ``k`` holds positions ``[k*bs, (k+1)*bs)``.
+* **Allocator.** Growth takes blocks from a free list, lowest ids first, so that a
+  session's blocks tend to form contiguous runs.  No byte is ever copied to grow.  An
+  evicted or dropped session returns its blocks.  Eviction is whole sessions in LRU
+  order, never the session being written, as in the reference.
+* **Validity, two policies.**
+  * ``truncate=True`` (default) is the reference's rule, bit for bit.  The scheduler
+    mirror and the worker reach the same decisions as with ``ShiftStore``: a start above
+    ``filled`` is refused as a hole, and a start at or below it drops everything above
+    the new top.  The blocks above are freed, not copied.
+  * ``truncate=False`` gives per-position validity: a sorted set of disjoint intervals.
+    A save marks its range valid and touches nothing else, holes are allowed, and
+    ``covers`` answers for every position of the range.  This is the store that
+    generation-0 reuse (no-resave) needs.
+* **Budget.** Counted in blocks actually held (``used`` = blocks x ``block_size``), not
+  in doubled capacity.  For the same sessions the block store evicts no more often than
+  the flat store.
+
+``read`` returns a gathered copy, since a block layout has no contiguous view.  The hot
+path never calls it: the loader reads the pool through the session's block table in the
+same launch that rotates (:meth:`table`, :meth:`pool`).
+"""
+
+from __future__ import annotations
+
+import bisect
+import heapq
+from collections import OrderedDict
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .shift_store import DEFAULT_STORE_TOKENS
+
+
+@dataclass
+class _BlockEntry:
+    table: list = field(default_factory=list)  # logical block -> pool block id (-1: none)
+    held: int = 0  # pool blocks this session owns
+    base: int = -1  # truncate policy: first position ever written (-1: nothing yet)
+    filled: int = 0  # truncate policy: [base, filled) holds valid KV
+    valid: list = field(default_factory=list)  # interval policy: sorted disjoint [lo, hi)
+    layers: set = field(default_factory=set)  # layers saved at least once
+
+
+def _add_interval(ivs: list, lo: int, hi: int) -> None:
+    """Insert ``[lo, hi)`` into sorted disjoint intervals, merging neighbours."""
+    i = bisect.bisect_left(ivs, (lo, lo))
+    if i > 0 and ivs[i - 1][1] >= lo:
+        i -= 1
+    j = i
+    while j < len(ivs) and ivs[j][0] <= hi:
+        lo, hi = min(lo, ivs[j][0]), max(hi, ivs[j][1])
+        j += 1
+    ivs[i:j] = [(lo, hi)]
+
+
+def _covered(ivs: list, lo: int, hi: int) -> bool:
+    i = bisect.bisect_right(ivs, (lo, float("inf"))) - 1
+    return i >= 0 and ivs[i][0] <= lo and hi <= ivs[i][1]
+
+
+class BlockShiftStore:
+    """Session-keyed KV in ``block_size``-token blocks of a per-layer device pool."""
+
+    def __init__(
+        self,
+        budget_tokens: int = DEFAULT_STORE_TOKENS,
+        device: str = "cuda",
+        allocate: bool = True,
+        block_size: int = 16,
+        truncate: bool = True,
+    ) -> None:
+        self.budget = int(budget_tokens)
+        self.block_size = int(block_size)
+        if self.block_size <= 0 or self.budget <= 0:
+            raise ValueError("budget_tokens and block_size must be positive")
+        self.pool_blocks = -(-self.budget // self.block_size)
+        self.device = device
+        self.allocate = allocate
+        self.truncate = bool(truncate)
+        self._sessions: OrderedDict[str, _BlockEntry] = OrderedDict()  # oldest first
+        self._free = list(range(self.pool_blocks))  # a heap: lowest id first
+        self._pools: dict[str, torch.Tensor] = {}
+        self.hits = 0
+        self.misses = 0
+        self.evictions = 0
+        self.refusals = 0
+        self.loaded_token_layers = 0
+        self.saved_token_layers = 0
+
+    # ----------------------------------------------------------------- internals
+
+    def _touch(self, session: str) -> _BlockEntry:
+        entry = self._sessions.get(session)
+        if entry is None:
+            entry = self._sessions[session] = _BlockEntry()
+        else:
+            self._sessions.move_to_end(session)
+        return entry
+
+    @property
+    def used(self) -> int:
+        return (self.pool_blocks - len(self._free)) * self.block_size
+
+    @property
+    def free_blocks(self) -> int:
+        return len(self._free)
+
+    def _release(self, entry: _BlockEntry, lo_block: int, hi_block: int) -> None:
+        for k in range(max(lo_block, 0), min(hi_block, len(entry.table))):
+            b = entry.table[k]
+            if b >= 0:
+                heapq.heappush(self._free, b)
+                entry.table[k] = -1
+                entry.held -= 1
+        while entry.table and entry.table[-1] < 0:
+            entry.table.pop()
+
+    def _ensure_blocks(self, session: str, entry: _BlockEntry, lo: int, hi: int) -> bool:
+        """Give ``session`` a block for every position in ``[lo, hi)``, evicting
+        least-recently-used other sessions when the free list runs short."""
+        bs = self.block_size
+        k0, k1 = lo // bs, -(-hi // bs)
+        if len(entry.table) < k1:
+            entry.table.extend([-1] * (k1 - len(entry.table)))
+        missing = [k for k in range(k0, k1) if entry.table[k] < 0]
+        while len(self._free) < len(missing):
+            victim = next((s for s in self._sessions if s != session), None)
+            if victim is None:
+                return False
+            self.drop(victim)
+            self.evictions += 1
+        for k in missing:
+            entry.table[k] = heapq.heappop(self._free)
+        entry.held += len(missing)
+        return True
+
+    # -------------------------------------------------------------------- public
+
+    def reserve(self, session: str, dst_start: int, n: int) -> bool:
+        """Make room for ``[dst_start, dst_start + n)``; False (nothing stored) when the
+        span cannot fit the budget or, under the truncate policy, would leave a hole
+        above ``filled``.  Idempotent (shift_store.py:177-199)."""
+        need = dst_start + n
+        entry = self._touch(session)
+        first = entry.base < 0 if self.truncate else not entry.valid
+        hole = self.truncate and not first and dst_start > entry.filled
+        if need > self.budget or n <= 0 or dst_start < 0 or hole:
+            self.refusals += 1
+            return False
+        if not self._ensure_blocks(session, entry, dst_start, need):
+            self.refusals += 1
+            return False
+        if self.truncate:
+            if first:
+                entry.base = dst_start
+            entry.filled = need
+            # everything above the new top is gone, as in the flat window: free it
+            self._release(entry, -(-need // self.block_size), len(entry.table))
+        else:
+            _add_interval(entry.valid, dst_start, need)
+        return True
+
+    def _holds(self, entry: _BlockEntry | None, start: int, n: int) -> bool:
+        if entry is None or n <= 0 or start < 0:
+            return False
+        if self.truncate:
+            return entry.base >= 0 and start >= entry.base and start + n <= entry.filled
+        return _covered(entry.valid, start, start + n)
+
+    def covers(self, session: str, start: int, n: int) -> bool:
+        """Whether ``[start, start + n)`` is held for ``session`` (counts a hit/miss)."""
+        ok = self._holds(self._sessions.get(session), start, n)
+        if ok:
+            self.hits += 1
+            self._touch(session)
+        else:
+            self.misses += 1
+        return ok
+
+    def pool(self, layer: str) -> torch.Tensor | None:
+        """The layer's pool ``[pool_blocks, block_size, heads, 2D]`` (None before any save)."""
+        return self._pools.get(layer)
+
+    def _pool_for(self, layer: str, row_shape, dtype, device) -> torch.Tensor:
+        p = self._pools.get(layer)
+        if p is None:
+            p = torch.zeros((self.pool_blocks, self.block_size, *row_shape), dtype=dtype,
+                            device=device)
+            self._pools[layer] = p
+        elif tuple(p.shape[2:]) != tuple(row_shape) or p.dtype != dtype:
+            raise ValueError(f"layer {layer}: rows {tuple(row_shape)} {dtype} do not match "
+                             f"the pool's {tuple(p.shape[2:])} {p.dtype}")
+        return p
+
+    def table(self, session: str) -> np.ndarray | None:
+        """The session's block table (int32, -1 where no block is held)."""
+        entry = self._sessions.get(session)
+        return None if entry is None else np.asarray(entry.table, dtype=np.int32)
+
+    def _positions_ok(self, entry: _BlockEntry | None, dst_start: int, n: int) -> bool:
+        if entry is None or not self.allocate or n <= 0 or dst_start < 0:
+            return False
+        bs = self.block_size
+        hi_block = -(-(dst_start + n) // bs)
+        return hi_block <= len(entry.table) and all(
+            entry.table[k] >= 0 for k in range(dst_start // bs, hi_block))
+
+    def write_target(
+        self, session: str, layer: str, dst_start: int, n: int, row_shape, dtype, device
+    ) -> torch.Tensor | None:
+        """The pool a device-side save of ``[dst_start, dst_start + n)`` writes into,
+        through :meth:`table`; None unless :meth:`reserve` gave the span its blocks.
+        Accounting as in :meth:`write`."""
+        entry = self._sessions.get(session)
+        if not self._positions_ok(entry, dst_start, n):
+            return None
+        p = self._pool_for(layer, row_shape, dtype, device)
+        entry.layers.add(layer)
+        self.saved_token_layers += n
+        return p
+
+    def write(self, session: str, layer: str, dst_start: int, src: torch.Tensor) -> None:
+        """Copy ``src`` ``[n, heads, 2D]`` into the session's blocks (shift_store.py:225-236)."""
+        n = src.shape[0]
+        p = self.write_target(session, layer, dst_start, n, src.shape[1:], src.dtype, self.device)
+        if p is None:
+            return
+        blk, off = self._rows(session, dst_start, n, p.device)
+        p[blk, off] = src.to(p.device, non_blocking=True)
+
+    def _rows(self, session: str, start: int, n: int, device):
+        pos = torch.arange(start, start + n, dtype=torch.int64)
+        tab = torch.as_tensor(self.table(session), dtype=torch.int64)
+        return tab[pos // self.block_size].to(device), (pos % self.block_size).to(device)
+
+    def lookup(self, session: str, layer: str, start: int, n: int) -> bool:
+        """:meth:`read`'s check and accounting without the gather: what a load calls once
+        per (load, layer) (vllm_shift_connector.py:506-513)."""
+        entry = self._sessions.get(session)
+        if not self._holds(entry, start, n) or layer not in entry.layers:
+            return False
+        self.loaded_token_layers += n
+        self._touch(session)
+        return True
+
+    def read(self, session: str, layer: str, start: int, n: int) -> torch.Tensor | None:
+        """``[n, heads, 2D]`` rows of ``[start, start + n)`` (a gathered copy), or None
+        where any position is not held (shift_store.py:238-250)."""
+        if not self.lookup(session, layer, start, n):
+            return None
+        p = self._pools[layer]
+        blk, off = self._rows(session, start, n, p.device)
+        return p[blk, off]
+
+    def drop(self, session: str) -> None:
+        entry = self._sessions.pop(session, None)
+        if entry is not None:
+            self._release(entry, 0, len(entry.table))
+
+    def stats(self) -> dict:
+        def held(e: _BlockEntry) -> int:
+            if self.truncate:
+                return max(e.filled - max(e.base, 0), 0)
+            return sum(hi - lo for lo, hi in e.valid)
+
+        return {
+            "budget_tokens": self.budget,
+            "used_tokens": self.used,
+            "pool_blocks": self.pool_blocks,
+            "free_blocks": len(self._free),
+            "sessions": {s: held(e) for s, e in self._sessions.items()},
+            "hits": self.hits,
+            "misses": self.misses,
+            "evictions": self.evictions,
+            "refusals": self.refusals,
+            "loaded_token_layers": self.loaded_token_layers,
+            "saved_token_layers": self.saved_token_layers,
+        }

@@ -10,6 +10,16 @@ every load x every layer, sources read straight out of each session's store buff
 
 Also here, as host logic: the layout detection of ``register_kv_caches`` (:393-402) and
 the multi-segment block alignment of ``_accept_multi`` (:225-245).
+
+Slots on the device.  The reference's scheduler builds every load's and save's int64
+slot list on the host (``slots()``, :349-366 / :320) and the worker copies it H2D
+(:504): 8 bytes per token.  A :class:`Load` or :class:`Save` built with ``from_blocks``
+carries the request's block table and a position range instead.  The kernel's plan pass
+turns positions into slots on the device (``MKV_ADDR_TABLE``), so the host ships 4
+bytes per 16 tokens.  Either store works as the source or target: the reference's flat
+:class:`~marathon_amd.shift_store.ShiftStore`, or the
+:class:`~marathon_amd.block_store.BlockShiftStore` pool, read and written through its
+block tables.
 """
 
 from __future__ import annotations
@@ -22,7 +32,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .shift_store import ShiftStore
+from .block_store import BlockShiftStore
+from .shift_store import ShiftStore, slots as host_slots
 from .spans import CacheSet, ShiftPlan
 
 logger = logging.getLogger("marathon_amd.shift")
@@ -31,21 +42,91 @@ logger = logging.getLogger("marathon_amd.shift")
 @dataclass
 class Save:
     """One save of a step (vllm_shift_connector.py:143-151): the positions this step
-    computed, ``slots`` in the paged cache, stored from ``dst_start``."""
+    computed, ``slots`` in the paged cache, stored from ``dst_start``.
+
+    ``Save.from_blocks`` leaves ``slots`` None: the paged rows are then positions
+    ``[dst_start, dst_start + n_tokens)`` through ``block_ids``, resolved on the device.
+    """
 
     session: str
-    slots: torch.Tensor  # int64 [T]
+    slots: torch.Tensor | None  # int64 [T]
     dst_start: int
+    block_ids: object = None  # the request's block table (device-side slots)
+    n_tokens: int = 0
+
+    @classmethod
+    def from_blocks(cls, session: str, block_ids, lo: int, hi: int) -> "Save":
+        return cls(session, None, int(lo), block_ids, int(hi) - int(lo))
+
+    @property
+    def n(self) -> int:
+        return int(self.slots.numel()) if self.slots is not None else max(int(self.n_tokens), 0)
+
+    @property
+    def paged_pos(self) -> int:
+        return int(self.dst_start)
 
 
 @dataclass
 class Load:
-    """One load of a step (vllm_shift_connector.py:135-140)."""
+    """One load of a step (vllm_shift_connector.py:135-140).
+
+    ``Load.from_blocks`` leaves ``slots`` None: the destination is then positions
+    ``[dst_start, dst_start + n_tokens)`` through ``block_ids``, resolved on the device.
+    """
 
     session: str
-    slots: torch.Tensor  # int64 [T]: destination slots of positions [lo, hi)
+    slots: torch.Tensor | None  # int64 [T]: destination slots of positions [lo, hi)
     src_start: int  # first source position in the session's store
     delta: int
+    block_ids: object = None  # the request's block table (device-side slots)
+    dst_start: int = 0
+    n_tokens: int = 0
+
+    @classmethod
+    def from_blocks(cls, session: str, block_ids, lo: int, hi: int, delta: int) -> "Load":
+        return cls(session, None, int(lo) - int(delta), int(delta), block_ids, int(lo),
+                   int(hi) - int(lo))
+
+    @property
+    def n(self) -> int:
+        return int(self.slots.numel()) if self.slots is not None else max(int(self.n_tokens), 0)
+
+    @property
+    def paged_pos(self) -> int:
+        return int(self.dst_start)
+
+
+def paged_index(items: list, block_size: int):
+    """Address the paged side of a batch of loads or saves: ``(mode, index, rows)``.
+
+    When no item carries host slots, the block tables are concatenated (int32) and each
+    item gets ``(pos, offset)``: position ``pos + i`` resolves through
+    ``table[offset + (pos + i) // block_size]`` on the device.  Otherwise the slots are
+    concatenated (int64; ``from_blocks`` items are expanded on the host) and each item
+    gets ``(0, offset)`` into them.
+    """
+    if all(it.slots is None for it in items):
+        tabs, rows, off = [], [], 0
+        for it in items:
+            t = np.asarray(it.block_ids, dtype=np.int32).reshape(-1)
+            if it.paged_pos < 0 or it.paged_pos + it.n > t.size * block_size:
+                raise ValueError(f"positions [{it.paged_pos}, {it.paged_pos + it.n}) exceed "
+                                 f"a block table of {t.size} blocks")
+            tabs.append(t)
+            rows.append((it.paged_pos, off))
+            off += t.size
+        return "table", torch.from_numpy(np.concatenate(tabs)), rows
+    parts, rows, off = [], [], 0
+    for it in items:
+        if it.slots is None:
+            sl = host_slots(it.block_ids, it.paged_pos, it.paged_pos + it.n, block_size)
+        else:
+            sl = it.slots.to(torch.int64).reshape(-1)
+        parts.append(sl)
+        rows.append((0, off))
+        off += int(sl.numel())
+    return "slots", torch.cat(parts), rows
 
 
 def detect_hnd(shape, block_size: int) -> bool:
@@ -86,7 +167,7 @@ class ShiftLoader:
 
     def __init__(
         self,
-        store: ShiftStore,
+        store: ShiftStore | BlockShiftStore,
         block_size: int,
         inv_freq: torch.Tensor,
         *,
@@ -116,26 +197,25 @@ class ShiftLoader:
     def start_load_kv(self, loads: list) -> int:
         """Issue every load of the step as one launch; returns token-layers loaded.
 
-        Mirrors :481-534: each (load, layer) source is ``store.read`` (so the store's
-        counters and LRU order move exactly as in the reference), and a load whose
-        source is missing for any layer is logged and ends the step's loading.
-        Divergence: the reference has already written the layers before the missing
-        one when it stops; here a missed load writes nothing.
+        Mirrors :481-534: each (load, layer) source is checked through the store (its
+        ``read`` accounting: counters and LRU order move exactly as in the reference),
+        and a load whose source is missing for any layer is logged and ends the step's
+        loading.  Divergence: the reference has already written the layers before the
+        missing one when it stops; here a missed load writes nothing.
         """
         if not loads or not self._kv:
             return 0
         names = list(self._kv)
+        blocky = isinstance(self.store, BlockShiftStore)
         groups: dict[str, int] = {}
-        rows = []
-        slot_parts = []
-        offset = 0
+        taken = []
         for load in loads:
-            n = int(load.slots.numel())
+            n = load.n
             if n == 0:
                 continue
             missing = None
             for name in names:
-                if self.store.read(load.session, name, load.src_start, n) is None:
+                if not self.store.lookup(load.session, name, load.src_start, n):
                     missing = name
                     break
             if missing is not None:
@@ -143,29 +223,48 @@ class ShiftLoader:
                     "shift: session %s has no stored KV for %s; load skipped", load.session, missing
                 )
                 break
-            g = groups.setdefault(load.session, len(groups))
-            rows.append((load.src_start, 0, 0, offset, n, int(load.delta), g, 0))
-            slot_parts.append(load.slots.to(torch.int64).reshape(-1))
-            offset += n
-        if not rows:
+            groups.setdefault(load.session, len(groups))
+            taken.append(load)
+        if not taken:
             return 0
-        src = CacheSet(
-            [[self.store.buffer(s, name) for name in names] for s in groups], "flat"
-        )
+        dst_mode, dst_index, dst_rows = paged_index(taken, self.block_size)
+        rows = []
+        if blocky:
+            # one pool per layer; each session's block table is the source index
+            tab_off, tabs, off = {}, [], 0
+            for sess in groups:
+                t = self.store.table(sess)
+                tab_off[sess] = off
+                tabs.append(t)
+                off += t.size
+            src = CacheSet([[self.store.pool(name) for name in names]], "nhd",
+                           self.store.block_size)
+            src_mode, src_index = "table", torch.from_numpy(np.concatenate(tabs))
+            for load, (dpos, didx) in zip(taken, dst_rows):
+                rows.append((load.src_start, dpos, tab_off[load.session], didx, load.n,
+                             int(load.delta), 0, 0))
+        else:
+            src = CacheSet(
+                [[self.store.buffer(sess, name) for name in names] for sess in groups], "flat"
+            )
+            src_mode, src_index = "flat", None
+            for load, (dpos, didx) in zip(taken, dst_rows):
+                rows.append((load.src_start, dpos, 0, didx, load.n, int(load.delta),
+                             groups[load.session], 0))
         dst = CacheSet([[self._kv[name] for name in names]], "hnd" if self.hnd else "nhd",
                        self.block_size)
         k_scale = None
         if dst.first.dtype == torch.float8_e4m3fn:
             k_scale = torch.tensor([float(self.k_scales.get(name, 1.0)) for name in names])
-        spans = np.array(rows, dtype=_lib.SPAN_DTYPE)
         plan = ShiftPlan(
-            spans,
+            np.array(rows, dtype=_lib.SPAN_DTYPE),
             src,
             dst,
             inv_freq=self.inv_freq,
-            src_mode="flat",
-            dst_mode="slots",
-            dst_index=torch.cat(slot_parts),
+            src_mode=src_mode,
+            src_index=src_index,
+            dst_mode=dst_mode,
+            dst_index=dst_index,
             k_scale=k_scale,
         )
         t0 = 0.0
@@ -174,18 +273,19 @@ class ShiftLoader:
             t0 = time.perf_counter()
         plan.launch()
         self.last_plan = plan
+        tokens = sum(load.n for load in taken)
         if self.timing:
             torch.cuda.synchronize(dst.first.device)
             ms = (time.perf_counter() - t0) * 1e3
             logger.info(
                 "shift: %d loads, %d tokens x %d layers, copy_ms=%.3f (%.1f GB/s)",
                 len(rows),
-                offset,
+                tokens,
                 len(names),
                 ms,
                 plan.algorithmic_bytes / 1e9 / max(ms / 1e3, 1e-12),
             )
-        return offset * len(names)
+        return tokens * len(names)
 
 
 class ShiftSaver:
@@ -196,9 +296,11 @@ class ShiftSaver:
     copies it into the store buffer (``ShiftStore.write``, shift_store.py:225-236).
     Here the gather kernel reads the paged rows and writes them straight into each
     session's buffer (delta 0: a pure copy), one launch for every save of the call.
+    With a :class:`BlockShiftStore`, the rows land in the layer's pool through the
+    session's block table, so a save never reallocates and never copies what is stored.
     """
 
-    def __init__(self, store: ShiftStore, block_size: int):
+    def __init__(self, store: ShiftStore | BlockShiftStore, block_size: int):
         self.store = store
         self.block_size = int(block_size)
         self.last_plan: ShiftPlan | None = None
@@ -207,11 +309,12 @@ class ShiftSaver:
         first = caches[0]
         hnd = detect_hnd(first.shape, self.block_size)
         row_shape = (first.shape[1] if hnd else first.shape[2], first.shape[3])
+        blocky = isinstance(self.store, BlockShiftStore)
         groups: dict[str, int] = {}
         bufs: list[list] = []
-        rows, slot_parts, offset = [], [], 0
+        taken = []
         for save in saves:
-            n = int(save.slots.numel())
+            n = save.n
             if n == 0:
                 continue
             # mirrors the scheduler's reserve for this step; idempotent across layers
@@ -227,23 +330,46 @@ class ShiftSaver:
                 bufs.append(targets)
             else:
                 bufs[g] = targets  # a save may have grown (reallocated) the buffers
-            rows.append((0, int(save.dst_start), offset, 0, n, 0, 0, g))
-            slot_parts.append(save.slots.to(torch.int64).reshape(-1))
-            offset += n
-        if not rows:
+            taken.append(save)
+        if blocky:
+            # a later save of the same call may have truncated an earlier one's blocks
+            taken = [sv for sv in taken
+                     if self.store._positions_ok(self.store._sessions.get(sv.session),
+                                                 sv.dst_start, sv.n)]
+        if not taken:
             return 0
+        src_mode, src_index, src_rows = paged_index(taken, self.block_size)
+        rows = []
+        if blocky:
+            tab_off, tabs, off = {}, [], 0
+            for sess in groups:
+                t = self.store.table(sess)
+                tab_off[sess] = off
+                tabs.append(t)
+                off += t.size
+            dst = CacheSet([[self.store.pool(name) for name in names]], "nhd",
+                           self.store.block_size)
+            dst_mode, dst_index = "table", torch.from_numpy(np.concatenate(tabs))
+            for sv, (spos, sidx) in zip(taken, src_rows):
+                rows.append((spos, int(sv.dst_start), sidx, tab_off[sv.session], sv.n, 0, 0, 0))
+        else:
+            dst = CacheSet(bufs, "flat")
+            dst_mode, dst_index = "flat", None
+            for sv, (spos, sidx) in zip(taken, src_rows):
+                rows.append((spos, int(sv.dst_start), sidx, 0, sv.n, 0, 0, groups[sv.session]))
         plan = ShiftPlan(
             np.array(rows, dtype=_lib.SPAN_DTYPE),
             CacheSet([caches], "hnd" if hnd else "nhd", self.block_size),
-            CacheSet(bufs, "flat"),
+            dst,
             inv_freq=None,
-            src_mode="slots",
-            src_index=torch.cat(slot_parts),
-            dst_mode="flat",
+            src_mode=src_mode,
+            src_index=src_index,
+            dst_mode=dst_mode,
+            dst_index=dst_index,
         )
         plan.launch()
         self.last_plan = plan
-        return offset * len(names)
+        return sum(sv.n for sv in taken) * len(names)
 
     def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, saves: list) -> int:
         """One layer, every save of the step (the reference's per-layer hook)."""

@@ -180,17 +180,23 @@ class ShiftStore:
         buf[dst_start : dst_start + n] = src.to(buf.device, non_blocking=True)
         self.saved_token_layers += n
 
-    def read(self, session: str, layer: str, start: int, n: int) -> torch.Tensor | None:
-        """The view ``buf[start:start + n]``, or None outside ``[base, filled)``."""
+    def lookup(self, session: str, layer: str, start: int, n: int) -> bool:
+        """:meth:`read`'s check and accounting without making the view: what a batched
+        load calls once per (load, layer) (vllm_shift_connector.py:506-513)."""
         entry = self._sessions.get(session)
         if entry is None or entry.base < 0 or start < entry.base or start + n > entry.filled:
-            return None
-        buf = entry.layers.get(layer)
-        if buf is None:
-            return None
+            return False
+        if entry.layers.get(layer) is None:
+            return False
         self.loaded_token_layers += n
         self._touch(session)  # same LRU order as the scheduler mirror's covers()
-        return buf[start : start + n]
+        return True
+
+    def read(self, session: str, layer: str, start: int, n: int) -> torch.Tensor | None:
+        """The view ``buf[start:start + n]``, or None outside ``[base, filled)``."""
+        if not self.lookup(session, layer, start, n):
+            return None
+        return self._sessions[session].layers[layer][start : start + n]
 
     def buffer(self, session: str, layer: str) -> torch.Tensor | None:
         """The whole ``[capacity, heads, 2D]`` buffer (what a batched load reads)."""

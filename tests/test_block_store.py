@@ -1,0 +1,321 @@
+"""The block-layout store (marathon_amd.block_store) on the CPU.
+
+* Under ``truncate=True`` it must reach the flat store's decisions exactly: the
+  reference's store tests (tests/test_shift_store.py, cited per case) are restated on
+  it, and a random operation sequence is replayed on both stores side by side.
+* The allocator: lowest ids first, no block held twice, drop and eviction return
+  blocks, growth never moves stored rows.
+* Under ``truncate=False`` validity is per position.  In the no-resave session that
+  the flat window corrupts (docs/single-request-load.md, "Design 2"), no load loses its
+  source.  A second failure that no store policy fixes is pinned as well: fresh saves
+  at their own index landing on drifted generation-0 bytes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from marathon_amd.block_store import BlockShiftStore
+from marathon_amd.remap import Remap, loads_for
+from marathon_amd.shift_store import ShiftStore, plan_load
+
+
+def _kv(n, value, heads=2, dim=4):
+    return torch.full((n, heads, dim), float(value))
+
+
+def _store(**kw):
+    kw.setdefault("budget_tokens", 4096)
+    kw.setdefault("device", "cpu")
+    return BlockShiftStore(**kw)
+
+
+def _check_allocator(st: BlockShiftStore):
+    held = [b for e in st._sessions.values() for b in e.table if b >= 0]
+    assert len(held) == len(set(held)), "a block is held twice"
+    assert sorted(held + list(st._free)) == list(range(st.pool_blocks))
+    for e in st._sessions.values():
+        assert e.held == sum(b >= 0 for b in e.table)
+
+
+# ------------------------------------------------- the reference's store cases
+
+
+def test_append_only_saves_extend_the_filled_span():  # :62-67
+    st = _store()
+    assert st.reserve("a", 0, 100) and st.reserve("a", 100, 50)
+    assert st.covers("a", 0, 150) and not st.covers("a", 0, 151)
+
+
+def test_a_save_that_would_leave_a_hole_is_refused():  # :70-75
+    st = _store()
+    st.reserve("a", 0, 100)
+    assert not st.reserve("a", 200, 10)
+    assert st.covers("a", 0, 100) and st.refusals == 1
+
+
+def test_an_edit_truncates_everything_above_it():  # :78-84
+    st = _store()
+    st.reserve("a", 0, 500)
+    free_before = st.free_blocks
+    assert st.reserve("a", 100, 50)
+    assert st.covers("a", 0, 150) and not st.covers("a", 0, 151)
+    # the blocks above the new top went back to the pool, nothing was copied
+    assert st.free_blocks == free_before + (-(-500 // 16) - -(-150 // 16))
+    _check_allocator(st)
+
+
+def test_a_span_larger_than_the_budget_is_refused():  # :87-90
+    st = _store(budget_tokens=1000)
+    assert not st.reserve("a", 0, 1001)
+    assert st.refusals == 1
+
+
+def test_reserve_is_idempotent():  # :93-97
+    st = _store()
+    for _ in range(3):
+        assert st.reserve("a", 0, 64)
+    assert st.covers("a", 0, 64) and st.used == 64
+    _check_allocator(st)
+
+
+def test_write_read_round_trip_and_session_isolation():  # :103-113
+    st = _store()
+    st.reserve("a", 0, 40)
+    st.reserve("b", 0, 40)
+    st.write("a", "l0", 0, _kv(40, 1.0))
+    st.write("b", "l0", 0, _kv(40, 2.0))
+    assert torch.equal(st.read("a", "l0", 0, 40), _kv(40, 1.0))
+    assert torch.equal(st.read("b", "l0", 0, 40), _kv(40, 2.0))
+    assert st.read("a", "l1", 0, 40) is None  # a layer never saved
+
+
+def test_read_past_the_filled_span_returns_none():  # :116-120
+    st = _store()
+    st.reserve("a", 0, 10)
+    st.write("a", "l0", 0, _kv(10, 1.0))
+    assert st.read("a", "l0", 5, 6) is None
+    assert st.read("a", "l0", 5, 5) is not None
+
+
+def test_growth_keeps_stored_rows_in_place():  # :123-130
+    st = _store()
+    st.reserve("a", 0, 20)
+    rows = torch.arange(20 * 2 * 4, dtype=torch.float32).reshape(20, 2, 4)
+    st.write("a", "l0", 0, rows)
+    pool, table = st.pool("l0"), st.table("a").copy()
+    ptr = pool.data_ptr()
+    st.reserve("a", 20, 3000)
+    st.write("a", "l0", 20, _kv(3000, 7.0))
+    assert st.pool("l0").data_ptr() == ptr  # never reallocated
+    assert np.array_equal(st.table("a")[: table.size], table)  # old blocks kept
+    assert torch.equal(st.read("a", "l0", 0, 20), rows)
+
+
+def test_lru_evicts_the_least_recently_used_session():  # :136-145
+    st = _store(budget_tokens=3 * 512)
+    for s in "abc":
+        assert st.reserve(s, 0, 512)
+    assert st.covers("a", 0, 512)  # a is now most recent; b is the oldest
+    assert st.reserve("d", 0, 512)
+    assert "b" not in st.stats()["sessions"] and st.evictions == 1
+    _check_allocator(st)
+
+
+def test_eviction_never_takes_the_session_being_written():  # :148-154
+    st = _store(budget_tokens=1024)
+    assert st.reserve("a", 0, 512)
+    assert st.reserve("a", 512, 512)
+    assert st.evictions == 0 and st.covers("a", 0, 1024)
+
+
+def test_an_evicted_session_is_a_miss_not_a_wrong_load():  # :157-164
+    st = _store(budget_tokens=512)
+    st.reserve("a", 0, 512)
+    st.write("a", "l0", 0, _kv(512, 1.0))
+    st.reserve("b", 0, 512)
+    assert not st.covers("a", 0, 16) and st.read("a", "l0", 0, 16) is None
+
+
+def test_bookkeeping_only_mode_tracks_positions_without_tensors():  # :167-175
+    st = _store(allocate=False)
+    assert st.reserve("a", 0, 100)
+    st.write("a", "l0", 0, _kv(100, 1.0))
+    assert st.pool("l0") is None and st.covers("a", 0, 100)
+
+
+def test_stats_reports_tokens_per_session():  # :178-186
+    st = _store()
+    st.reserve("a", 0, 100)
+    st.reserve("b", 16, 50)
+    s = st.stats()
+    assert s["sessions"] == {"a": 100, "b": 50}
+    assert s["used_tokens"] == (7 + 4) * 16 and s["free_blocks"] == s["pool_blocks"] - 11
+
+
+def test_the_first_save_may_start_above_zero():  # :189-198
+    st = _store()
+    assert st.reserve("a", 300, 100)
+    assert st.covers("a", 300, 100) and not st.covers("a", 299, 2)
+    assert st.table("a")[: 300 // 16].tolist() == [-1] * (300 // 16)  # no blocks below
+
+
+def test_plan_load_runs_against_the_block_store():  # shift_store.py:282-315
+    st = _store(allocate=False)
+    st.reserve("s", 0, 1000)
+    d, why = plan_load(st, "s", {"dst_start": 64, "dst_end": 900, "delta": -30}, 64, 1200, 16)
+    assert why == "ok" and (d.lo, d.hi, d.delta) == (64, 896, -30)
+
+
+# ------------------------------------------------------------- the allocator
+
+
+def test_fresh_sessions_get_contiguous_lowest_blocks():
+    st = _store()
+    st.reserve("a", 0, 100)
+    st.reserve("b", 0, 40)
+    assert st.table("a").tolist() == list(range(7))
+    assert st.table("b").tolist() == [7, 8, 9]
+    st.drop("a")
+    st.reserve("c", 0, 20)
+    assert st.table("c").tolist() == [0, 1]  # lowest ids come back first
+    _check_allocator(st)
+
+
+def test_random_operations_keep_the_allocator_consistent():
+    rng = np.random.default_rng(5)
+    for truncate in (True, False):
+        st = _store(budget_tokens=2048, truncate=truncate, allocate=False)
+        for _ in range(3000):
+            s = "abcde"[int(rng.integers(5))]
+            op = rng.random()
+            if op < 0.7:
+                st.reserve(s, int(rng.integers(0, 1800)), int(rng.integers(1, 400)))
+            elif op < 0.95:
+                st.covers(s, int(rng.integers(0, 1800)), int(rng.integers(1, 400)))
+            else:
+                st.drop(s)
+        _check_allocator(st)
+
+
+# ------------------------------------------ truncate=True: the flat store's rules
+
+
+def test_truncate_policy_replays_the_flat_store_decisions():
+    """Same operations on both stores (a budget no sequence outgrows, since eviction
+    timing is the one documented difference): every return value and every window
+    agree, and every valid position has a block."""
+    rng = np.random.default_rng(7)
+    flat = ShiftStore(budget_tokens=1 << 16, device="cpu", allocate=False, slab=256)
+    blk = BlockShiftStore(budget_tokens=1 << 16, device="cpu", allocate=False)
+    for _ in range(5000):
+        s = "abcd"[int(rng.integers(4))]
+        op = rng.random()
+        start, n = int(rng.integers(-2, 3000)), int(rng.integers(-1, 500))
+        if op < 0.55:
+            if start < 0:
+                start = 0
+            assert flat.reserve(s, start, n) == blk.reserve(s, start, n), (s, start, n)
+        elif op < 0.97:
+            assert flat.covers(s, start, n) == blk.covers(s, start, n), (s, start, n)
+        else:
+            flat.drop(s)
+            blk.drop(s)
+        assert flat.stats()["sessions"] == blk.stats()["sessions"]
+    for s, e in blk._sessions.items():
+        lo, hi = max(e.base, 0), e.filled
+        for p in range(lo, hi):
+            assert e.table[p // 16] >= 0
+    assert flat.refusals == blk.refusals and flat.hits == blk.hits
+    _check_allocator(blk)
+
+
+# ----------------------------------------- truncate=False: per-position validity
+
+
+def test_interval_policy_allows_holes_and_never_truncates():
+    st = _store(truncate=False)
+    assert st.reserve("a", 0, 100)
+    assert st.reserve("a", 300, 50)  # a hole: allowed
+    assert st.covers("a", 300, 50) and not st.covers("a", 90, 20)
+    assert st.reserve("a", 20, 10)  # a save below the top truncates nothing
+    assert st.covers("a", 0, 100) and st.covers("a", 300, 50)
+    assert st.reserve("a", 100, 200)  # filling the hole joins the intervals
+    assert st.covers("a", 0, 350) and st.stats()["sessions"]["a"] == 350
+
+
+def _no_resave_session(truncate: bool, turns=20, seed=0):
+    """A paged session under no-resave (src/marathon/server.py:267-276), shaped like the
+    pager: every turn demotes the oldest live message to a stub, reuses everything after
+    it through the generation-0 book, and appends a user message plus a reply.  Only
+    what was computed this turn is saved, at its own positions.
+
+    Returns ``(lost, overwritten)``: loaded positions whose source the store no longer
+    holds, and loaded positions the store holds but whose bytes were written over by a
+    later save at the same index.
+    """
+    rng = np.random.default_rng(seed)
+    st = BlockShiftStore(budget_tokens=1 << 15, device="cpu", truncate=truncate)
+    next_id = [1000]
+
+    def fresh(n):
+        ids = list(range(next_id[0], next_id[0] + n))
+        next_id[0] += n
+        return ids
+
+    def save(lo, ids):
+        if ids and st.reserve("s", lo, len(ids)):
+            st.write("s", "l0", lo, torch.tensor(ids, dtype=torch.float32).reshape(-1, 1, 1))
+
+    msgs = [fresh(int(rng.integers(150, 300))) for _ in range(12)]
+    live = 0  # the oldest message not demoted yet
+    text = [t for m in msgs for t in m]
+    save(0, text)
+    book, lost, overwritten = Remap(), 0, 0
+    for _ in range(turns):
+        at = sum(len(m) for m in msgs[:live])
+        old_len = len(msgs[live])
+        msgs[live] = fresh(int(rng.integers(5, 20)))
+        live += 1
+        delta = len(msgs[live - 1]) - old_len
+        reused_hi = len(text) + delta  # everything after the stub, before the new text
+        msgs.append(fresh(int(rng.integers(20, 60))))  # the new user message
+        text = [t for m in msgs for t in m]
+        lo = at + len(msgs[live - 1])
+        for ld in loads_for(book, [{"dst_start": lo, "dst_end": reused_hi, "delta": delta}]):
+            src, n = ld["dst_start"] - ld["delta"], ld["dst_end"] - ld["dst_start"]
+            want = torch.tensor(text[ld["dst_start"]:ld["dst_end"]], dtype=torch.float32)
+            if not st.covers("s", src, n):
+                lost += n
+                continue
+            overwritten += int((st.read("s", "l0", src, n).reshape(-1) != want).sum())
+        book = book.after_turn([(lo, reused_hi, delta)], len(text))
+        save(at, msgs[live - 1])  # the stub, at its own positions
+        save(reused_hi, text[reused_hi:])  # the new user message
+        reply = fresh(int(rng.integers(10, 40)))
+        msgs[-1] = msgs[-1] + reply
+        save(len(text), reply)
+        text = text + reply
+    return lost, overwritten
+
+
+def test_per_position_validity_keeps_what_truncation_loses():
+    """The measured blocker (docs/single-request-load.md, "Design 2"): under the flat
+    window, the stub saved low in the history truncates the generation-0 bytes above it,
+    and later loads find their source gone.  Per-position validity loses nothing."""
+    lost_flat, _ = _no_resave_session(truncate=True)
+    lost_blocks, _ = _no_resave_session(truncate=False)
+    assert lost_flat > 0
+    assert lost_blocks == 0
+
+
+def test_fresh_saves_at_their_own_index_can_overwrite_generation_zero_bytes():
+    """What per-position validity does not fix.  After the text shrinks, the new text
+    appended at its own indices lands where a drifted span's generation-0 bytes still
+    live.  A later load then reads the wrong tokens with every position "valid".  So
+    generation-0 reuse also needs fresh KV stored away from every drifted span's
+    source.  This is a property of the address book, not of any store; it is pinned
+    here so the limit stays visible."""
+    _, overwritten = _no_resave_session(truncate=False)
+    assert overwritten > 0

@@ -15,7 +15,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from marathon_amd import ShiftStore, plan_load, plan_save, slots
+from marathon_amd import BlockShiftStore, ShiftStore, plan_load, plan_save, slots
 from marathon_amd.connector import Load, Save, ShiftLoader, ShiftSaver
 from marathon_amd.shift_kernels import inv_freq_for
 
@@ -28,8 +28,9 @@ FILLER = "deterministic filler that makes a message worth several blocks of toke
 class RealKVEngine:
     """A paged KV cache with block-level prefix caching, driven by the real decisions."""
 
-    def __init__(self, dev, blocks=1024, seed=0):
+    def __init__(self, dev, blocks=1024, seed=0, store="flat", device_slots=False):
         self.dev = dev
+        self.device_slots = device_slots
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         self.table_k = torch.randn(256, H, D, dtype=torch.float64, device=dev, generator=g)
@@ -38,7 +39,10 @@ class RealKVEngine:
         self.inv64 = self.inv.to(dev, torch.float64)
         self.kv = {f"layer{i}": torch.zeros(blocks, H, BS, 2 * D, dtype=torch.bfloat16, device=dev)
                    for i in range(LAYERS)}
-        self.store = ShiftStore(budget_tokens=1 << 16, device=str(dev), slab=1024)
+        if store == "flat":
+            self.store = ShiftStore(budget_tokens=1 << 16, device=str(dev), slab=1024)
+        else:
+            self.store = BlockShiftStore(budget_tokens=1 << 14, device=str(dev), block_size=BS)
         self.loader = ShiftLoader(self.store, BS, self.inv)
         self.loader.register_kv_caches(self.kv)
         self.saver = ShiftSaver(self.store, BS)
@@ -104,7 +108,9 @@ class RealKVEngine:
             params["save"] = True
         lo, hi = window
         sl = slots(blocks, lo, hi, BS)
-        self.saver.save_all(self.kv, [Save(session, sl, lo)])
+        sv = Save.from_blocks(session, list(blocks), lo, hi) if self.device_slots else Save(
+            session, sl, lo)
+        assert self.saver.save_all(self.kv, [sv]) == (hi - lo) * LAYERS
         st = self.store_shifts.setdefault(session, torch.zeros(1 << 16, dtype=torch.int32))
         st[lo:hi] = self.shifts[sl]
 
@@ -116,7 +122,12 @@ class RealKVEngine:
             self.declines.append(why)
         if decision is not None:
             sl = slots(blocks, decision.lo, decision.hi, BS)
-            self.loader.start_load_kv([Load(session, sl, decision.src_start, decision.delta)])
+            if self.device_slots:
+                ld = Load.from_blocks(session, list(blocks), decision.lo, decision.hi,
+                                      decision.delta)
+            else:
+                ld = Load(session, sl, decision.src_start, decision.delta)
+            assert self.loader.start_load_kv([ld]) == len(sl) * LAYERS
             st = self.store_shifts[session]
             self.shifts[sl] = st[decision.src_start:decision.src_start + len(sl)] + int(
                 decision.delta != 0)
@@ -154,12 +165,14 @@ def _phases(load, n_prompt):
     return [(lo, None), (n_prompt, {"dst_start": lo, "dst_end": hi, "delta": load["delta"]})]
 
 
-def test_front_edits_through_the_real_kernels(gpu):
-    eng = RealKVEngine(gpu)
+@pytest.mark.parametrize("store,device_slots", [
+    ("flat", False), ("flat", True), ("blocks", False), ("blocks", True)])
+def test_front_edits_through_the_real_kernels(gpu, store, device_slots):
+    eng = RealKVEngine(gpu, store=store, device_slots=device_slots)
     messages, keep_last, turns = [], 3, 9
     prompt_pieces = None  # pieces of the previous request's prompt: what the store holds
     for t in range(turns):
-        print(f"case session turn {t}", flush=True)
+        print(f"case session store={store} device_slots={device_slots} turn {t}", flush=True)
         load = None
         if t >= keep_last:
             d = t - keep_last
@@ -215,3 +228,50 @@ def test_saver_matches_a_torch_gather(gpu):
                 want = src[s // BS, s % BS]
                 got = store.read(sv.session, name, sv.dst_start, s.numel())
                 assert torch.equal(got, want), (hnd, name, sv.session)
+
+
+def test_block_store_saver_and_loader_match_torch(gpu):
+    """Saves into the block store's pool (host slots and block tables), read back
+    through the store, then a load out of the pool: bytes equal a torch gather."""
+    g = torch.Generator(device=gpu)
+    g.manual_seed(7)
+    kv = {f"l{i}": torch.randn(64, H, BS, 2 * D, device=gpu, generator=g).to(torch.bfloat16)
+          for i in range(3)}
+    store = BlockShiftStore(budget_tokens=4096, device=str(gpu), block_size=BS)
+    saver = ShiftSaver(store, BS)
+    perm = torch.randperm(64).tolist()
+    print("case block store saves", flush=True)
+    assert store.reserve("b", 0, 16)  # "b" holds [0, 16) already
+    sa = Save("a", slots(perm[:20], 5, 5 + 300, BS), 0)
+    sb = Save.from_blocks("b", perm[20:], 16, 16 + 200)
+    assert saver.save_all(kv, [sa, sb]) == 500 * 3
+    torch.cuda.synchronize(gpu)
+    for name, cache in kv.items():
+        src = cache.permute(0, 2, 1, 3)
+        for sess, sl, start in (("a", sa.slots, 0), ("b", slots(perm[20:], 16, 216, BS), 16)):
+            s = sl.to(gpu)
+            assert torch.equal(store.read(sess, name, start, s.numel()), src[s // BS, s % BS])
+    print("case block store load, rotated", flush=True)
+    out = {name: torch.zeros_like(c) for name, c in kv.items()}
+    loader = ShiftLoader(store, BS, inv_freq_for(D, 1e6))
+    loader.register_kv_caches(out)
+    dst_blocks = torch.randperm(64).tolist()
+    n = loader.start_load_kv([Load.from_blocks("a", dst_blocks, 37, 37 + 250, 37),
+                              Load.from_blocks("b", dst_blocks, 300, 300 + 100, 290)])
+    assert n == 350 * 3
+    torch.cuda.synchronize(gpu)
+    for name, cache in out.items():
+        for sess, lo, hi, delta in (("a", 37, 287, 37), ("b", 300, 400, 290)):
+            s = slots(dst_blocks, lo, hi, BS).to(gpu)
+            got = cache[s // BS, :, s % BS]
+            want = store.read(sess, name, lo - delta, hi - lo)
+            assert torch.equal(got[..., D:], want[..., D:])  # V bit-exact
+            # K: rotated by delta, within the reference rotation's rounding of the input
+            k0 = want[..., :D].to(torch.float64)
+            ang = float(delta) * inv_freq_for(D, 1e6).to(gpu, torch.float64)
+            emb = torch.cat((ang, ang))
+            rot = torch.cat((-k0[..., D // 2:], k0[..., : D // 2]), -1)
+            ref = k0 * emb.cos() + rot * emb.sin()
+            pair = torch.maximum(k0.abs(), torch.roll(k0, D // 2, -1).abs())
+            assert bool(((got[..., :D].to(torch.float64) - ref).abs()
+                         <= 2.0**-8 * (ref.abs() + 2 * pair) + 1e-6).all())

@@ -251,3 +251,22 @@ def test_accept_multi_block_aligns_and_drops_what_it_cannot_serve():
 )
 def test_layout_detection(shape, hnd):  # vllm_shift_connector.py:396-402
     assert detect_hnd(shape, 16) is hnd
+
+
+def test_paged_index_tables_and_slots():
+    """Device-side slots: block tables concatenated with per-item offsets; a batch with
+    any host slots falls back to concatenated int64 slots (from_blocks items expanded)."""
+    from marathon_amd.connector import Load, Save, paged_index
+
+    a = Load.from_blocks("s", [7, 3, 9], 5, 40, -2)
+    b = Load.from_blocks("t", [1, 2], 16, 32, 4)
+    mode, index, rows = paged_index([a, b], 16)
+    assert mode == "table" and index.tolist() == [7, 3, 9, 1, 2]
+    assert rows == [(5, 0), (16, 3)]
+    assert (a.src_start, a.n, b.src_start, b.n) == (7, 35, 12, 16)
+    c = Load("u", slots([4], 0, 3, 16), 0, 0)
+    mode, index, rows = paged_index([a, c], 16)
+    assert mode == "slots" and rows == [(0, 0), (0, 35)]
+    assert index.tolist() == slots([7, 3, 9], 5, 40, 16).tolist() + [64, 65, 66]
+    with pytest.raises(ValueError):
+        paged_index([Save.from_blocks("s", [1, 2], 20, 40)], 16)  # 40 > 2 blocks
