@@ -202,6 +202,78 @@ def other_configs(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def connector_step(dev, steps: int, warmup: int) -> dict:
+    """Worker load steps through the connector: a session held in the block-layout store,
+    loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
+    slot lists) into an HND paged cache.  Times the whole call from Python (store
+    checks, span table, one pinned upload, plan + shift kernels) to the stream's
+    completion, next to the kernels alone on the same plan.  Two steps: config 3's eight
+    spans, and one 29,232-token load, the size of the reference's in-engine measurement
+    (docs/findings.md:664-666: 34.4 ms copy_ms, 6.2 ms of it the kernel)."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import BlockShiftStore
+    from marathon_amd import workloads as W
+    from marathon_amd.connector import Load, ShiftLoader
+    from marathon_amd.shift_kernels import inv_freq_for
+
+    layers, heads, d, bs = 40, 8, 128, 16
+    lay = W.config3_layout()
+    history = lay.src_history
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    store = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
+    assert store.reserve("s", 0, history)
+    names = [f"layer{i}" for i in range(layers)]
+    for name in names:
+        store.write_target("s", name, 0, history, (heads, 2 * d), torch.bfloat16,
+                           dev).normal_(generator=gen)
+    blocks = -(-max(lay.dst_history, history) // bs) + 8
+    kv = {name: torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
+          for name in names}
+    table = np.random.default_rng(1).permutation(blocks).astype(np.int32)
+    loader = ShiftLoader(store, bs, inv_freq_for(d, 1e6))
+    loader.register_kv_caches(kv)
+    cases = {
+        "config3_8_spans": lambda: [
+            Load.from_blocks("s", table, int(dst), int(dst) + int(n), int(dl))
+            for dst, n, dl in zip(lay.dst_start, lay.length, lay.delta)],
+        "one_load_29232_tokens": lambda: [Load.from_blocks("s", table, 0, 29232, -186)],
+    }
+    out = {"what": "ShiftLoader.start_load_kv from a BlockShiftStore session into an HND "
+           "paged cache (40 layers, bf16), block tables on the device; medians over steps",
+           "reference_in_engine_copy_ms_29232_tokens": 34.4,
+           "reference_kernel_ms_29232_tokens": 6.2}
+    for case, loads in cases.items():
+        for _ in range(warmup):
+            loader.start_load_kv(loads())
+        torch.cuda.synchronize()
+        host, e2e = [], []
+        for _ in range(steps):
+            batch = loads()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            loader.start_load_kv(batch)
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            e2e.append((time.perf_counter() - t0) * 1e3)
+            host.append((t1 - t0) * 1e3)
+        plan = loader.last_plan
+        _, per = time_plan(plan, steps, warmup, torch.cuda.current_stream(dev))
+        kms = float(np.mean(per))
+        out[case] = {
+            "tokens": plan.tokens,
+            "ms_end_to_end": round(float(np.median(e2e)), 4),
+            "host_ms": round(float(np.median(host)), 4),
+            "kernel_ms": round(kms, 4),
+            "kernel_GB_s": round(plan.algorithmic_bytes / (kms / 1e3) / 1e9, 1),
+        }
+    del store, kv, loader
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +283,8 @@ def main() -> int:
     ap.add_argument("--no-reference-shape", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the informational timings of configs 2, 4 and 5")
+    ap.add_argument("--no-connector-step", action="store_true",
+                    help="skip the end-to-end connector load step timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (for PMC counter scaling)")
     args = ap.parse_args()
@@ -269,6 +343,9 @@ def main() -> int:
         extra["reference_shape"] = reference_shape(dev, max(5, args.steps // 2), args.warmup, stream)
     if not args.no_other_configs:
         extra["other_configs"] = other_configs(dev, max(5, args.steps // 2), args.warmup, stream)
+    if not args.no_connector_step:
+        log("connector load step (block store, device-side slots)")
+        extra["connector_step"] = connector_step(dev, max(5, args.steps), args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (reference torch path on the host, config 1)")

@@ -28,8 +28,10 @@ memory layout:
     the new top.  The blocks above are freed, not copied.
   * ``truncate=False`` gives per-position validity: a sorted set of disjoint intervals.
     A save marks its range valid and touches nothing else, holes are allowed, and
-    ``covers`` answers for every position of the range.  This is the store that
-    generation-0 reuse (no-resave) needs.
+    ``covers`` answers for every position of the range.  Generation-0 reuse
+    (no-resave) needs this.  It is not sufficient on its own: after the text shrinks,
+    new text saved at its own index can land on a drifted span's generation-0 bytes,
+    so fresh KV must also be placed away from every drifted span's source.
 * **Budget.** Counted in blocks actually held (``used`` = blocks x ``block_size``), not
   in doubled capacity.  For the same sessions the block store evicts no more often than
   the flat store.
@@ -263,6 +265,24 @@ class BlockShiftStore:
         self.loaded_token_layers += n
         self._touch(session)
         return True
+
+    def lookup_layers(self, session: str, layers, start: int, n: int):
+        """:meth:`lookup` of every layer in order, with the same accounting; returns the
+        first layer that misses, or None when all hit."""
+        entry = self._sessions.get(session)
+        if not self._holds(entry, start, n):
+            return next(iter(layers), None)
+        hit = 0
+        try:
+            for layer in layers:
+                if layer not in entry.layers:
+                    return layer
+                self.loaded_token_layers += n
+                hit += 1
+            return None
+        finally:
+            if hit:
+                self._touch(session)  # the LRU order one touch per layer would leave
 
     def read(self, session: str, layer: str, start: int, n: int) -> torch.Tensor | None:
         """``[n, heads, 2D]`` rows of ``[start, start + n)`` (a gathered copy), or None

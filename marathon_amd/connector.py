@@ -108,14 +108,20 @@ def paged_index(items: list, block_size: int):
     """
     if all(it.slots is None for it in items):
         tabs, rows, off = [], [], 0
+        seen: dict[int, tuple] = {}  # items of one request share its block table
         for it in items:
-            t = np.asarray(it.block_ids, dtype=np.int32).reshape(-1)
-            if it.paged_pos < 0 or it.paged_pos + it.n > t.size * block_size:
+            hit = seen.get(id(it.block_ids))
+            if hit is None:
+                t = it.block_ids
+                t = t.cpu().numpy() if isinstance(t, torch.Tensor) else t
+                t = np.asarray(t, dtype=np.int32).reshape(-1)
+                hit = seen[id(it.block_ids)] = (off, t.size)
+                tabs.append(t)
+                off += t.size
+            if it.paged_pos < 0 or it.paged_pos + it.n > hit[1] * block_size:
                 raise ValueError(f"positions [{it.paged_pos}, {it.paged_pos + it.n}) exceed "
-                                 f"a block table of {t.size} blocks")
-            tabs.append(t)
-            rows.append((it.paged_pos, off))
-            off += t.size
+                                 f"a block table of {hit[1]} blocks")
+            rows.append((it.paged_pos, hit[0]))
         return "table", torch.from_numpy(np.concatenate(tabs)), rows
     parts, rows, off = [], [], 0
     for it in items:
@@ -190,6 +196,9 @@ class ShiftLoader:
         shape = next(iter(self._kv.values())).shape
         self.hnd = detect_hnd(shape, self.block_size)
         self.head_size = shape[3] // 2
+        self._dst = CacheSet([list(self._kv.values())], "hnd" if self.hnd else "nhd",
+                             self.block_size)
+        self._pool_set: tuple | None = None  # (pool ids, CacheSet) of a block store
         one = next(iter(self._kv.values()))
         if one.is_cuda:
             _lib.lib()  # the kernels are compiled ahead of time: only load the library
@@ -213,11 +222,7 @@ class ShiftLoader:
             n = load.n
             if n == 0:
                 continue
-            missing = None
-            for name in names:
-                if not self.store.lookup(load.session, name, load.src_start, n):
-                    missing = name
-                    break
+            missing = self.store.lookup_layers(load.session, names, load.src_start, n)
             if missing is not None:
                 logger.error(
                     "shift: session %s has no stored KV for %s; load skipped", load.session, missing
@@ -237,8 +242,11 @@ class ShiftLoader:
                 tab_off[sess] = off
                 tabs.append(t)
                 off += t.size
-            src = CacheSet([[self.store.pool(name) for name in names]], "nhd",
-                           self.store.block_size)
+            pools = [self.store.pool(name) for name in names]
+            key = tuple(id(p) for p in pools)
+            if self._pool_set is None or self._pool_set[0] != key:
+                self._pool_set = (key, CacheSet([pools], "nhd", self.store.block_size))
+            src = self._pool_set[1]
             src_mode, src_index = "table", torch.from_numpy(np.concatenate(tabs))
             for load, (dpos, didx) in zip(taken, dst_rows):
                 rows.append((load.src_start, dpos, tab_off[load.session], didx, load.n,
@@ -251,8 +259,7 @@ class ShiftLoader:
             for load, (dpos, didx) in zip(taken, dst_rows):
                 rows.append((load.src_start, dpos, 0, didx, load.n, int(load.delta),
                              groups[load.session], 0))
-        dst = CacheSet([[self._kv[name] for name in names]], "hnd" if self.hnd else "nhd",
-                       self.block_size)
+        dst = self._dst
         k_scale = None
         if dst.first.dtype == torch.float8_e4m3fn:
             k_scale = torch.tensor([float(self.k_scales.get(name, 1.0)) for name in names])

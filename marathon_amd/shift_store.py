@@ -192,6 +192,24 @@ class ShiftStore:
         self._touch(session)  # same LRU order as the scheduler mirror's covers()
         return True
 
+    def lookup_layers(self, session: str, layers, start: int, n: int):
+        """:meth:`lookup` of every layer in order, with the same accounting; returns the
+        first layer that misses, or None when all hit."""
+        entry = self._sessions.get(session)
+        if entry is None or entry.base < 0 or start < entry.base or start + n > entry.filled:
+            return next(iter(layers), None)
+        hit = 0
+        try:
+            for layer in layers:
+                if entry.layers.get(layer) is None:
+                    return layer
+                self.loaded_token_layers += n
+                hit += 1
+            return None
+        finally:
+            if hit:
+                self._touch(session)  # the LRU order one touch per layer would leave
+
     def read(self, session: str, layer: str, start: int, n: int) -> torch.Tensor | None:
         """The view ``buf[start:start + n]``, or None outside ``[base, filled)``."""
         if not self.lookup(session, layer, start, n):

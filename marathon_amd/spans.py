@@ -97,13 +97,43 @@ class CacheSet:
         return t.shape[0] * (1 if self.layout == "flat" else self.block_size)
 
 
+class _Staging:
+    """Host arrays bound for the device, packed into one pinned buffer and copied with
+    one asynchronous H2D: the host never waits for the stream to drain."""
+
+    ALIGN = 256
+
+    def __init__(self) -> None:
+        self.parts: list = []
+        self.size = 0
+
+    def add(self, a: np.ndarray) -> int:
+        a = np.ascontiguousarray(a)
+        off = self.size
+        self.parts.append((off, a))
+        self.size = off + (a.nbytes + self.ALIGN - 1) // self.ALIGN * self.ALIGN
+        return off
+
+    def upload(self, device) -> torch.Tensor:
+        host = torch.empty(max(self.size, self.ALIGN), dtype=torch.uint8, pin_memory=True)
+        view = host.numpy()
+        for off, a in self.parts:
+            view[off:off + a.nbytes] = a.reshape(-1).view(np.uint8)
+        # the caching host allocator keeps ``host`` until this copy has completed
+        return host.to(device, non_blocking=True)
+
+
 class ShiftPlan:
     """A batched shift, resident on the device and launchable any number of times.
 
     ``spans``: a ``SPAN_DTYPE`` structured array (or anything ``np.asarray`` turns into
     one).  ``src_index`` / ``dst_index``: int64 slots (mode ``slots``), int32 block ids
-    (mode ``table``) or ``None`` (mode ``flat``).  ``inv_freq``: fp32 [rotary / 2].
-    ``k_scale``: fp32 [layers] for fp8 caches.
+    (mode ``table``) or ``None`` (mode ``flat``), on the host or the device.
+    ``inv_freq``: fp32 [rotary / 2].  ``k_scale``: fp32 [layers] for fp8 caches.
+
+    Everything host-side (span table, per-(group, layer) base addresses, host index
+    arrays, tables) goes to the device in one pinned, stream-ordered copy, so building
+    a plan never blocks on the GPU.
     """
 
     def __init__(
@@ -134,30 +164,52 @@ class ShiftPlan:
         self.tokens = int(np.maximum(spans["n_tokens"], 0).sum()) if self.n_spans else 0
         self.dtype = dtype_code(dst.first.dtype)
         self._keep: list = []
-        dev = self.device
+        stage = _Staging()
 
-        def upload(a: np.ndarray) -> torch.Tensor:
-            t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
-            self._keep.append(t)
-            return t
+        def place(t: torch.Tensor | None, dtype: torch.dtype, np_dtype):
+            """A device tensor is used in place; a host one is staged.  Returns
+            ``(device tensor or None, staging offset or None, count)``."""
+            if t is None:
+                return None, None, 0
+            t = t.detach().reshape(-1)
+            if t.is_cuda:
+                t = t.to(device=self.device, dtype=dtype).contiguous()
+                self._keep.append(t)
+                return t, None, t.numel()
+            a = t.numpy() if t.dtype == dtype else t.to(dtype).numpy()
+            return None, stage.add(a.astype(np_dtype, copy=False)), a.size
 
         self.rotary = 0 if inv_freq is None else 2 * int(inv_freq.numel())
-        inv_dev = None
-        if inv_freq is not None:
-            inv_dev = inv_freq.detach().to(device=dev, dtype=torch.float32).contiguous()
-            self._keep.append(inv_dev)
-        scale_dev = None
+        inv = place(inv_freq, torch.float32, np.float32)
+        scale = (None, None, 0)
         if self.dtype == _lib.MKV_FP8_E4M3 and self.rotary:
             if k_scale is None:
                 raise ValueError("fp8 caches need k_scale [layers]")
-            scale_dev = k_scale.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
-            if scale_dev.numel() < dst.layers:
+            scale = place(k_scale, torch.float32, np.float32)
+            if scale[2] < dst.layers:
                 raise ValueError("k_scale needs one entry per layer")
-            self._keep.append(scale_dev)
 
-        src_side = self._side(src, src_mode, src_index, upload)
-        dst_side = self._side(dst, dst_mode, dst_index, upload)
-        span_bytes = upload(spans.view(np.uint8).reshape(-1)) if self.n_spans else None
+        src_plan = self._side(src, src_mode, src_index, stage, place)
+        dst_plan = self._side(dst, dst_mode, dst_index, stage, place)
+        span_off = stage.add(spans.view(np.uint8).reshape(-1)) if self.n_spans else None
+        with torch.cuda.device(self.device):
+            blob = stage.upload(self.device)
+            # launches on another stream first wait for this copy (see launch)
+            self._build_stream = torch.cuda.current_stream(self.device)
+            self._ready = torch.cuda.Event()
+            self._ready.record(self._build_stream)
+        self._keep.append(blob)
+        self._synced = {int(self._build_stream.cuda_stream)}
+        base = blob.data_ptr()
+
+        def ptr(item) -> int | None:
+            t, off, _ = item
+            if t is not None:
+                return t.data_ptr()
+            return None if off is None else base + off
+
+        src_side = self._finish_side(src_plan, ptr)
+        dst_side = self._finish_side(dst_plan, ptr)
 
         self.descs = []
         step = _lib.MKV_MAX_SPANS
@@ -170,15 +222,15 @@ class ShiftPlan:
             default=0,
         )
         # one workspace serves every chunk: the chunks run in stream order
-        self.workspace = torch.empty(max(int(need), 16), dtype=torch.uint8, device=dev)
+        self.workspace = torch.empty(max(int(need), 16), dtype=torch.uint8, device=self.device)
         for lo, cnt in chunks:
             d = _lib.ShiftDesc()
-            d.spans = span_bytes.data_ptr() + lo * _lib.SPAN_DTYPE.itemsize
+            d.spans = base + span_off + lo * _lib.SPAN_DTYPE.itemsize
             d.workspace = self.workspace.data_ptr()
             d.workspace_bytes = self.workspace.numel()
             d.total_tokens = int(counts[lo:lo + cnt].sum())
-            d.inv_freq = inv_dev.data_ptr() if inv_dev is not None else None
-            d.k_scale = scale_dev.data_ptr() if scale_dev is not None else None
+            d.inv_freq = ptr(inv)
+            d.k_scale = ptr(scale)
             d.error_flags = None
             d.n_spans = cnt
             d.layers = dst.layers
@@ -190,34 +242,47 @@ class ShiftPlan:
             d.dst = dst_side
             self.descs.append(d)
 
-    def _side(self, cs: CacheSet, mode: str, index, upload) -> _lib.Side:
+    @staticmethod
+    def _side(cs: CacheSet, mode: str, index, stage: _Staging, place) -> dict:
         if mode not in MODES:
             raise ValueError(f"mode {mode!r}")
         eb = cs.first.element_size()
-        hs = cs.head_size
         k = np.array([[t.data_ptr() for t in row] for row in cs.caches], dtype=np.uint64)
-        v = k + np.uint64(hs * eb)
-        side = _lib.Side()
-        side.k_base = upload(k.reshape(-1).view(np.int64)).data_ptr()
-        side.v_base = upload(v.reshape(-1).view(np.int64)).data_ptr()
+        v = k + np.uint64(cs.head_size * eb)
         caps = np.array([cs.slots_of(row[0]) for row in cs.caches], dtype=np.int64)
-        side.num_slots = int(caps.min())
-        side.group_slots = None if np.all(caps == caps[0]) else upload(caps).data_ptr()
-        if mode == "flat":
-            side.index = None
-            side.index_len = 0
-        else:
+        out = {
+            "cs": cs,
+            "mode": mode,
+            "k": (None, stage.add(k.reshape(-1)), k.size),
+            "v": (None, stage.add(v.reshape(-1)), v.size),
+            "num_slots": int(caps.min()),
+            "group_slots": None if np.all(caps == caps[0]) else (None, stage.add(caps), caps.size),
+            "index": (None, None, 0),
+        }
+        if mode != "flat":
             if index is None:
                 raise ValueError(f"mode {mode!r} needs an index array")
-            want = torch.int64 if mode == "slots" else torch.int32
-            t = index.to(device=self.device, dtype=want).contiguous()
-            self._keep.append(t)
-            side.index = t.data_ptr() if t.numel() else None
-            side.index_len = t.numel()
+            if mode == "slots":
+                out["index"] = place(index, torch.int64, np.int64)
+            else:
+                out["index"] = place(index, torch.int32, np.int32)
+        return out
+
+    @staticmethod
+    def _finish_side(plan: dict, ptr) -> _lib.Side:
+        cs = plan["cs"]
+        side = _lib.Side()
+        side.k_base = ptr(plan["k"])
+        side.v_base = ptr(plan["v"])
+        side.num_slots = plan["num_slots"]
+        side.group_slots = None if plan["group_slots"] is None else ptr(plan["group_slots"])
+        n_index = plan["index"][2]
+        side.index = ptr(plan["index"]) if n_index else None
+        side.index_len = n_index
         bs, hstr, ostr = cs.strides
         side.block_stride, side.head_stride, side.offset_stride = bs, hstr, ostr
         side.block_size = cs.block_size
-        side.mode = MODES[mode]
+        side.mode = MODES[plan["mode"]]
         side.groups = cs.groups
         return side
 
@@ -234,6 +299,13 @@ class ShiftPlan:
             stream = current_stream(self.device)
         L = _lib.lib()
         with torch.cuda.device(self.device):
+            if int(stream) not in self._synced:
+                # the tables were copied on the stream current at build time
+                ext = torch.cuda.ExternalStream(int(stream), device=self.device)
+                ext.wait_event(self._ready)
+                for t in (*self._keep, self.workspace):
+                    t.record_stream(ext)
+                self._synced.add(int(stream))
             for d in self.descs:
                 d.error_flags = error_flags.data_ptr() if error_flags is not None else None
                 _lib.check(L.mkv_shift_spans(ctypes.byref(d), ctypes.c_void_p(stream)))

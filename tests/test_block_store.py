@@ -319,3 +319,26 @@ def test_fresh_saves_at_their_own_index_can_overwrite_generation_zero_bytes():
     here so the limit stays visible."""
     _, overwritten = _no_resave_session(truncate=False)
     assert overwritten > 0
+
+
+def test_lookup_layers_matches_per_layer_lookups():
+    """The loader's bulk check leaves the same counters and LRU order as one lookup per
+    layer, on both stores."""
+    for make in (lambda: ShiftStore(budget_tokens=4096, device="cpu"),
+                 lambda: _store()):
+        a, b = make(), make()
+        for st in (a, b):
+            for s in ("x", "y"):
+                st.reserve(s, 0, 100)
+                st.write(s, "l0", 0, _kv(100, 1.0))
+                st.write(s, "l1", 0, _kv(100, 1.0))
+        names = ["l0", "l1", "l2"]
+        for sess, start, n in (("x", 0, 50), ("y", 10, 90), ("x", 60, 50), ("z", 0, 5)):
+            miss_a = a.lookup_layers(sess, names[:2], start, n)
+            miss_b = next((nm for nm in names[:2] if not b.lookup(sess, nm, start, n)), None)
+            assert miss_a == miss_b
+            miss_a = a.lookup_layers(sess, names, start, n)
+            miss_b = next((nm for nm in names if not b.lookup(sess, nm, start, n)), None)
+            assert miss_a == miss_b
+            assert a.stats() == b.stats()
+            assert list(a._sessions) == list(b._sessions)
