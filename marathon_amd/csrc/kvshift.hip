@@ -56,6 +56,13 @@
 #define MKV_PASSES_1B 4
 #endif
 
+// 1: store V before rotating K (frees its registers during the rotation).  Measured
+// 11% slower for bf16: a row's K and V halves are adjacent, and writing them far apart
+// in time costs write efficiency.  Off.
+#ifndef MKV_V_FIRST
+#define MKV_V_FIRST 0
+#endif
+
 #ifndef MKV_WG_THREADS
 #define MKV_WG_THREADS 256
 #endif
@@ -249,10 +256,6 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
   return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xFFFFu)));
 }
 
-__device__ __forceinline__ float clamp448(float q) {
-  return q > 448.0f ? 448.0f : (q < -448.0f ? -448.0f : q);
-}
-
 // Rotate the C elements of one 16-byte chunk.  `mine` is this lane's K chunk,
 // `part` the partner chunk (same element positions, other half of the rotation),
 // c / s the cos and signed sin of those positions.
@@ -324,44 +327,54 @@ __device__ __forceinline__ bool has_nan_code(uint32_t w) {
 
 template <>
 struct Rotor<MKV_FP8_E4M3> {
+  // y / scale, correctly rounded, clamped to the format's range.  A NaN comes out as
+  // 448 here (IEEE minNum/maxNum return the other operand); run() rewrites it.
+  static __device__ __forceinline__ float quant(float y, float scale, float rcp) {
+    const float q0 = y * rcp;
+    const float r = __builtin_fmaf(-q0, scale, y);
+    const float q = __builtin_copysignf(__builtin_fmaf(r, rcp, q0), y);
+    return __builtin_fmaxf(__builtin_fminf(q, 448.0f), -448.0f);
+  }
+  static __device__ __forceinline__ void decode4(uint32_t w, float* out) {
+    const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+    out[0] = lo[0];
+    out[1] = lo[1];
+    out[2] = hi[0];
+    out[3] = hi[1];
+  }
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
                                               const float* s, float scale, float rcp) {
-    float q[16];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const f2 m01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(mine[w]), false);
-      const f2 m23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(mine[w]), true);
-      const f2 p01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(part[w]), false);
-      const f2 p23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(part[w]), true);
-      const float mk[4] = {m01[0], m01[1], m23[0], m23[1]};
-      const float pk[4] = {p01[0], p01[1], p23[0], p23[1]};
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int e = 4 * w + b;
-        const float x = mk[b] * scale;
-        const float xp = pk[b] * scale;
-        const float y = rot1(x, xp, c[e], s[e]);
-        const float q0 = y * rcp;
-        const float r = __builtin_fmaf(-q0, scale, y);
-        q[e] = clamp448(__builtin_copysignf(__builtin_fmaf(r, rcp, q0), y));
-      }
-    }
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      int v = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * w], q[4 * w + 1], 0, false);
-      v = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * w + 2], q[4 * w + 3], v, true);
+      float mk[4], pk[4], q[4];
+      decode4(mine[w], mk);
+      decode4(part[w], pk);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int e = 4 * w + b;
+        q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale, rcp);
+      }
+      int v = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+      v = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], v, true);
       out[w] = static_cast<uint32_t>(v);
     }
     const bool any_nan = has_nan_code(mine[0]) | has_nan_code(mine[1]) | has_nan_code(mine[2]) |
                          has_nan_code(mine[3]) | has_nan_code(part[0]) | has_nan_code(part[1]) |
                          has_nan_code(part[2]) | has_nan_code(part[3]);
     if (__builtin_expect(any_nan, 0)) {
+      // y is NaN exactly when an input of its rotation is (every other input is finite)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        if (q[e] != q[e]) {
-          const int sh = 8 * (e & 3);
-          out[e >> 2] = (out[e >> 2] & ~(0xFFu << sh)) | (0x7Fu << sh);
+      for (int w = 0; w < 4; ++w) {
+        float mk[4], pk[4];
+        decode4(mine[w], mk);
+        decode4(part[w], pk);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int e = 4 * w + b;
+          const float y = rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]);
+          if (y != y) out[w] = (out[w] & ~(0xFFu << (8 * b))) | (0x7Fu << (8 * b));
         }
       }
     }
@@ -686,7 +699,14 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- phase C: rotate K (the whole wave joins the partner exchange)
+    // ---- phase C: V goes out as it came in, then K is rotated (the whole wave joins
+    // the partner exchange)
+#if MKV_V_FIRST
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (live[u] && lane_live) store16(dbv[u] + d_at[u] + d_lane, vd[u]);
+    }
+#endif
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool wave_rotates = UNIFORM ? (live[u] && delta_u[u] != 0 && p.rotary > 0)
@@ -718,7 +738,9 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
     for (int u = 0; u < U; ++u) {
       if (live[u] && lane_live) {
         store16(dbk[u] + d_at[u] + d_lane, kd[u]);
+#if !MKV_V_FIRST
         store16(dbv[u] + d_at[u] + d_lane, vd[u]);
+#endif
       }
     }
   }
