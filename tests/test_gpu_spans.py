@@ -14,8 +14,9 @@ import torch
 from marathon_amd import ShiftStore, slots
 from marathon_amd import workloads as W
 from marathon_amd.connector import Load, ShiftLoader
+from marathon_amd.spans import span_array
 from oracle import kvshift_oracle as orc
-from tests.helpers import bits, inv_freq, oracle_side, oracle_spans
+from tests.helpers import bits, dname, inv_freq, oracle_side, oracle_spans
 
 pytestmark = pytest.mark.gpu
 
@@ -119,3 +120,110 @@ def test_connector_loader_end_to_end(gpu):
             orc.scatter_shifted(src_rows, want, ld.slots.numpy(), bs, True, ld.delta,
                                 inv_freq().numpy(), "bf16")
         assert np.array_equal(bits(kv[name]), want), name
+
+
+def _two_session_plan(gpu, dtype, heads, d, rotary, seed, spans, table, k_scale=None,
+                      fill=None):
+    """Two flat sessions (300 and 200 rows) -> an HND paged cache addressed through a
+    block table; returns (plan, dst caches)."""
+    from marathon_amd.spans import CacheSet, ShiftPlan, span_array
+    from tests.helpers import randn
+
+    g = torch.Generator().manual_seed(seed)
+    layers, bs = 2, 16
+    sc = 0.05
+    bufs = [[randn((n, heads, 2 * d), dtype, g, sc).to(gpu) for _ in range(layers)]
+            for n in (300, 200)]
+    kv = [(randn((48, heads, bs, 2 * d), dtype, g, sc) if fill is None else fill).to(gpu)
+          for _ in range(layers)]
+    plan = ShiftPlan(span_array(spans), CacheSet(bufs, "flat"), CacheSet([kv], "hnd", bs),
+                     inv_freq=inv_freq(rotary), src_mode="flat", dst_mode="table",
+                     dst_index=torch.tensor(table, dtype=torch.int32), k_scale=k_scale)
+    return plan, kv
+
+
+@pytest.mark.parametrize("dtype,heads,d,rotary", [
+    (torch.float16, 6, 128, 128),
+    (torch.float32, 5, 128, 64),
+    (torch.bfloat16, 3, 64, 64),
+    (torch.bfloat16, 5, 256, 128),
+    (torch.float8_e4m3fn, 5, 128, 128),
+])
+def test_batched_other_geometries_match_oracle(gpu, dtype, heads, d, rotary):
+    """Non-uniform head counts (a wave pass spans tokens), partial rotary, fp16 / fp32 /
+    fp8, a table-addressed destination: every destination byte against the oracle."""
+    print(f"case batched geometry {dtype} heads={heads} d={d} rotary={rotary}", flush=True)
+    table = torch.randperm(48, generator=torch.Generator().manual_seed(3)).tolist()
+    spans = [(5, 3, 0, 0, 120, -41, 0, 0),    # session 0, positions 3..123
+             (150, 130, 0, 0, 140, 1999, 0, 0),
+             (0, 300, 0, 0, 190, 0, 1, 0),     # session 1, delta 0: a plain copy
+             (17, 520, 0, 0, 180, -7, 1, 0)]
+    k_scale = torch.tensor([0.037, 0.081]) if dtype == torch.float8_e4m3fn else None
+    plan, kv = _two_session_plan(gpu, dtype, heads, d, rotary, 11, spans, table, k_scale)
+    src_o = oracle_side(plan.src, "flat", None)
+    dst_o = oracle_side(plan.dst, "table", torch.tensor(table, dtype=torch.int32))
+    orc.shift_spans(oracle_spans(span_array(spans)), src_o, dst_o, inv_freq(rotary).numpy(),
+                    dname(dtype), None if k_scale is None else k_scale.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer, t in enumerate(kv):
+        assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
+
+
+def test_out_of_range_rows_are_flagged_and_skipped(gpu):
+    """Bad indices on either side never write: a -1 and a too-large block id in the
+    destination table, source positions past a session's rows, and a span naming a
+    group that does not exist.  Each raises its flag; every other row lands exactly as
+    in a plan that leaves the bad rows out."""
+    from marathon_amd import _lib
+
+    print("case out-of-range rows", flush=True)
+    table = torch.randperm(48, generator=torch.Generator().manual_seed(5)).tolist()
+    bad_table = list(table)
+    bad_table[2] = -1  # positions 32..47
+    bad_table[4] = 10**6  # positions 64..79
+    spans_bad = [(0, 20, 0, 0, 80, 33, 0, 0),       # dst 20..100 crosses blocks 2 and 4
+                 (190, 400, 0, 0, 20, -5, 1, 0),    # src 190..210, session 1 has 200 rows
+                 (0, 600, 0, 0, 30, 0, 7, 0)]       # group 7 does not exist
+    spans_ok = [(0, 20, 0, 0, 12, 33, 0, 0),        # 20..32
+                (28, 48, 0, 0, 16, 33, 0, 0),       # 48..64
+                (60, 80, 0, 0, 20, 33, 0, 0),       # 80..100
+                (190, 400, 0, 0, 10, -5, 1, 0)]     # src 190..200
+    fill = torch.full((48, 8, 16, 256), 3.0).to(torch.bfloat16)
+    plan_b, kv_b = _two_session_plan(gpu, torch.bfloat16, 8, 128, 128, 4, spans_bad,
+                                     bad_table, fill=fill)
+    plan_g, kv_g = _two_session_plan(gpu, torch.bfloat16, 8, 128, 128, 4, spans_ok, table,
+                                     fill=fill)
+    fb = torch.zeros(1, dtype=torch.int32, device=gpu)
+    fg = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan_b.launch(error_flags=fb)
+    plan_g.launch(error_flags=fg)
+    torch.cuda.synchronize(gpu)
+    assert int(fg.item()) == 0
+    want = _lib.MKV_FLAG_SRC_RANGE | _lib.MKV_FLAG_DST_RANGE | _lib.MKV_FLAG_SPAN
+    assert int(fb.item()) == want
+    for a, b in zip(kv_b, kv_g):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_single_span_out_of_range_slot_is_flagged_and_skipped(gpu):
+    from marathon_amd import _lib, rope_shift, scatter_shifted
+
+    print("case single-span out-of-range slot", flush=True)
+    g = torch.Generator().manual_seed(8)
+    src = torch.randn(40, 8, 256, generator=g).to(torch.bfloat16).to(gpu)
+    kv = torch.zeros(4, 8, 16, 256, dtype=torch.bfloat16, device=gpu)
+    kv_ok = kv.clone()
+    sl = torch.arange(40, dtype=torch.int64)
+    sl[7] = 64  # the cache holds 64 slots
+    sl[30] = -3
+    keep = torch.tensor([i not in (7, 30) for i in range(40)])
+    shift = rope_shift(123, 128, inv_freq(), gpu)
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    scatter_shifted(src, kv, sl.to(gpu), 16, True, shift, error_flags=flags)
+    scatter_shifted(src[keep.to(gpu)].contiguous(), kv_ok, sl[keep].to(gpu), 16, True, shift)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == _lib.MKV_FLAG_DST_RANGE
+    assert torch.equal(kv.view(torch.int16), kv_ok.view(torch.int16))
