@@ -274,6 +274,61 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     return out
 
 
+def save_step(dev, steps: int, warmup: int) -> dict:
+    """The save path (paged cache -> block-layout store) through ``ShiftSaver.save_all``:
+    an edit turn's one-shot ``save="full"`` re-gather of a 29,232-token prompt over 40
+    layers, and a decode step's one-token save (vllm_shift_connector.py:296-330,
+    :539-553).  Block tables on the device; whole call to stream completion, next to the
+    kernels alone."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import BlockShiftStore
+    from marathon_amd.connector import Save, ShiftSaver
+
+    layers, heads, d, bs, n = 40, 8, 128, 16, 29232
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    blocks = -(-n // bs) + 8
+    names = [f"layer{i}" for i in range(layers)]
+    kv = {name: torch.randn(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev,
+                            generator=gen) for name in names}
+    table = np.random.default_rng(2).permutation(blocks).astype(np.int32)
+    store = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
+    saver = ShiftSaver(store, bs)
+    out = {"what": "ShiftSaver.save_all from an HND paged cache (40 layers, bf16) into a "
+           "BlockShiftStore session, block tables on the device; medians over steps"}
+    cases = {"full_prompt_29232_tokens": lambda: [Save.from_blocks("s", table, 0, n)],
+             "decode_step_1_token": lambda: [Save.from_blocks("s", table, n - 1, n)]}
+    for case, saves in cases.items():
+        for _ in range(warmup):
+            saver.save_all(kv, saves())
+        torch.cuda.synchronize()
+        e2e, host = [], []
+        for _ in range(steps):
+            batch = saves()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            saver.save_all(kv, batch)
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            e2e.append((time.perf_counter() - t0) * 1e3)
+            host.append((t1 - t0) * 1e3)
+        plan = saver.last_plan
+        _, per = time_plan(plan, steps, warmup, torch.cuda.current_stream(dev))
+        kms = float(np.mean(per))
+        out[case] = {
+            "tokens": plan.tokens,
+            "ms_end_to_end": round(float(np.median(e2e)), 4),
+            "host_ms": round(float(np.median(host)), 4),
+            "kernel_ms": round(kms, 4),
+            "kernel_GB_s": round(plan.algorithmic_bytes / (kms / 1e3) / 1e9, 1),
+        }
+    del store, kv, saver
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,7 +339,7 @@ def main() -> int:
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the informational timings of configs 2, 4 and 5")
     ap.add_argument("--no-connector-step", action="store_true",
-                    help="skip the end-to-end connector load step timing")
+                    help="skip the end-to-end connector load and save step timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (for PMC counter scaling)")
     args = ap.parse_args()
@@ -346,6 +401,8 @@ def main() -> int:
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
         extra["connector_step"] = connector_step(dev, max(5, args.steps), args.warmup)
+        log("connector save step (paged -> block store)")
+        extra["save_step"] = save_step(dev, max(5, args.steps), args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (reference torch path on the host, config 1)")

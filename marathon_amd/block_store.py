@@ -54,9 +54,13 @@ import torch
 from .shift_store import DEFAULT_STORE_TOKENS
 
 
+def _no_blocks() -> np.ndarray:
+    return np.zeros(0, dtype=np.int32)
+
+
 @dataclass
 class _BlockEntry:
-    table: list = field(default_factory=list)  # logical block -> pool block id (-1: none)
+    table: np.ndarray = field(default_factory=_no_blocks)  # logical block -> pool id (-1: none)
     held: int = 0  # pool blocks this session owns
     base: int = -1  # truncate policy: first position ever written (-1: nothing yet)
     filled: int = 0  # truncate policy: [base, filled) holds valid KV
@@ -129,32 +133,33 @@ class BlockShiftStore:
         return len(self._free)
 
     def _release(self, entry: _BlockEntry, lo_block: int, hi_block: int) -> None:
-        for k in range(max(lo_block, 0), min(hi_block, len(entry.table))):
-            b = entry.table[k]
-            if b >= 0:
-                heapq.heappush(self._free, b)
-                entry.table[k] = -1
-                entry.held -= 1
-        while entry.table and entry.table[-1] < 0:
-            entry.table.pop()
+        part = entry.table[max(lo_block, 0):max(min(hi_block, entry.table.size), 0)]
+        freed = part[part >= 0]
+        for b in freed.tolist():
+            heapq.heappush(self._free, b)
+        entry.held -= int(freed.size)
+        part[:] = -1
+        live = np.flatnonzero(entry.table >= 0)
+        entry.table = entry.table[: int(live[-1]) + 1 if live.size else 0]
 
     def _ensure_blocks(self, session: str, entry: _BlockEntry, lo: int, hi: int) -> bool:
         """Give ``session`` a block for every position in ``[lo, hi)``, evicting
         least-recently-used other sessions when the free list runs short."""
         bs = self.block_size
         k0, k1 = lo // bs, -(-hi // bs)
-        if len(entry.table) < k1:
-            entry.table.extend([-1] * (k1 - len(entry.table)))
-        missing = [k for k in range(k0, k1) if entry.table[k] < 0]
-        while len(self._free) < len(missing):
+        if entry.table.size < k1:
+            entry.table = np.concatenate(
+                (entry.table, np.full(k1 - entry.table.size, -1, dtype=np.int32)))
+        missing = k0 + np.flatnonzero(entry.table[k0:k1] < 0)
+        while len(self._free) < missing.size:
             victim = next((s for s in self._sessions if s != session), None)
             if victim is None:
                 return False
             self.drop(victim)
             self.evictions += 1
-        for k in missing:
-            entry.table[k] = heapq.heappop(self._free)
-        entry.held += len(missing)
+        if missing.size:
+            entry.table[missing] = [heapq.heappop(self._free) for _ in range(missing.size)]
+        entry.held += int(missing.size)
         return True
 
     # -------------------------------------------------------------------- public
@@ -178,7 +183,7 @@ class BlockShiftStore:
                 entry.base = dst_start
             entry.filled = need
             # everything above the new top is gone, as in the flat window: free it
-            self._release(entry, -(-need // self.block_size), len(entry.table))
+            self._release(entry, -(-need // self.block_size), entry.table.size)
         else:
             _add_interval(entry.valid, dst_start, need)
         return True
@@ -216,17 +221,39 @@ class BlockShiftStore:
         return p
 
     def table(self, session: str) -> np.ndarray | None:
-        """The session's block table (int32, -1 where no block is held)."""
+        """The session's block table (int32, -1 where no block is held; read-only)."""
         entry = self._sessions.get(session)
-        return None if entry is None else np.asarray(entry.table, dtype=np.int32)
+        if entry is None:
+            return None
+        view = entry.table.view()
+        view.flags.writeable = False
+        return view
 
     def _positions_ok(self, entry: _BlockEntry | None, dst_start: int, n: int) -> bool:
         if entry is None or not self.allocate or n <= 0 or dst_start < 0:
             return False
         bs = self.block_size
         hi_block = -(-(dst_start + n) // bs)
-        return hi_block <= len(entry.table) and all(
-            entry.table[k] >= 0 for k in range(dst_start // bs, hi_block))
+        return hi_block <= entry.table.size and bool(
+            (entry.table[dst_start // bs:hi_block] >= 0).all())
+
+    def holds_blocks(self, session: str, dst_start: int, n: int) -> bool:
+        """Whether every position of ``[dst_start, dst_start + n)`` has a block."""
+        return self._positions_ok(self._sessions.get(session), dst_start, n)
+
+    def write_targets(
+        self, session: str, layers, dst_start: int, n: int, row_shape, dtype, device
+    ) -> list | None:
+        """:meth:`write_target` for several layers, the span checked once."""
+        entry = self._sessions.get(session)
+        if not self._positions_ok(entry, dst_start, n):
+            return None
+        out = []
+        for layer in layers:
+            out.append(self._pool_for(layer, row_shape, dtype, device))
+            entry.layers.add(layer)
+            self.saved_token_layers += n
+        return out
 
     def write_target(
         self, session: str, layer: str, dst_start: int, n: int, row_shape, dtype, device
@@ -234,13 +261,8 @@ class BlockShiftStore:
         """The pool a device-side save of ``[dst_start, dst_start + n)`` writes into,
         through :meth:`table`; None unless :meth:`reserve` gave the span its blocks.
         Accounting as in :meth:`write`."""
-        entry = self._sessions.get(session)
-        if not self._positions_ok(entry, dst_start, n):
-            return None
-        p = self._pool_for(layer, row_shape, dtype, device)
-        entry.layers.add(layer)
-        self.saved_token_layers += n
-        return p
+        got = self.write_targets(session, (layer,), dst_start, n, row_shape, dtype, device)
+        return None if got is None else got[0]
 
     def write(self, session: str, layer: str, dst_start: int, src: torch.Tensor) -> None:
         """Copy ``src`` ``[n, heads, 2D]`` into the session's blocks (shift_store.py:225-236)."""
@@ -253,7 +275,7 @@ class BlockShiftStore:
 
     def _rows(self, session: str, start: int, n: int, device):
         pos = torch.arange(start, start + n, dtype=torch.int64)
-        tab = torch.as_tensor(self.table(session), dtype=torch.int64)
+        tab = torch.from_numpy(self._sessions[session].table.astype(np.int64))
         return tab[pos // self.block_size].to(device), (pos % self.block_size).to(device)
 
     def lookup(self, session: str, layer: str, start: int, n: int) -> bool:
@@ -296,7 +318,7 @@ class BlockShiftStore:
     def drop(self, session: str) -> None:
         entry = self._sessions.pop(session, None)
         if entry is not None:
-            self._release(entry, 0, len(entry.table))
+            self._release(entry, 0, entry.table.size)
 
     def stats(self) -> dict:
         def held(e: _BlockEntry) -> int:

@@ -311,6 +311,15 @@ class ShiftSaver:
         self.store = store
         self.block_size = int(block_size)
         self.last_plan: ShiftPlan | None = None
+        self._sets: dict[str, tuple] = {}  # role -> (tensor ids, CacheSet)
+
+    def _cached(self, role: str, tensors: list, layout: str) -> CacheSet:
+        """The CacheSet of ``tensors``, rebuilt only when the tensors change."""
+        key = tuple(id(t) for t in tensors)
+        hit = self._sets.get(role)
+        if hit is None or hit[0] != key:
+            hit = self._sets[role] = (key, CacheSet([list(tensors)], layout, self.block_size))
+        return hit[1]
 
     def _plan(self, names: list, caches: list, saves: list) -> int:
         first = caches[0]
@@ -327,9 +336,9 @@ class ShiftSaver:
             # mirrors the scheduler's reserve for this step; idempotent across layers
             if not self.store.reserve(save.session, save.dst_start, n):
                 continue
-            targets = [self.store.write_target(save.session, name, save.dst_start, n, row_shape,
-                                               first.dtype, first.device) for name in names]
-            if any(t is None for t in targets):
+            targets = self.store.write_targets(save.session, names, save.dst_start, n,
+                                               row_shape, first.dtype, first.device)
+            if targets is None:
                 continue
             g = groups.get(save.session)
             if g is None:
@@ -340,9 +349,7 @@ class ShiftSaver:
             taken.append(save)
         if blocky:
             # a later save of the same call may have truncated an earlier one's blocks
-            taken = [sv for sv in taken
-                     if self.store._positions_ok(self.store._sessions.get(sv.session),
-                                                 sv.dst_start, sv.n)]
+            taken = [sv for sv in taken if self.store.holds_blocks(sv.session, sv.dst_start, sv.n)]
         if not taken:
             return 0
         src_mode, src_index, src_rows = paged_index(taken, self.block_size)
@@ -354,8 +361,7 @@ class ShiftSaver:
                 tab_off[sess] = off
                 tabs.append(t)
                 off += t.size
-            dst = CacheSet([[self.store.pool(name) for name in names]], "nhd",
-                           self.store.block_size)
+            dst = self._cached("pools", [self.store.pool(name) for name in names], "nhd")
             dst_mode, dst_index = "table", torch.from_numpy(np.concatenate(tabs))
             for sv, (spos, sidx) in zip(taken, src_rows):
                 rows.append((spos, int(sv.dst_start), sidx, tab_off[sv.session], sv.n, 0, 0, 0))
@@ -366,7 +372,7 @@ class ShiftSaver:
                 rows.append((spos, int(sv.dst_start), sidx, 0, sv.n, 0, 0, groups[sv.session]))
         plan = ShiftPlan(
             np.array(rows, dtype=_lib.SPAN_DTYPE),
-            CacheSet([caches], "hnd" if hnd else "nhd", self.block_size),
+            self._cached("paged", caches, "hnd" if hnd else "nhd"),
             dst,
             inv_freq=None,
             src_mode=src_mode,

@@ -241,6 +241,18 @@ class ShiftStore:
         self.saved_token_layers += n
         return buf
 
+    def write_targets(
+        self, session: str, layers, dst_start: int, n: int, row_shape, dtype, device
+    ) -> list | None:
+        """:meth:`write_target` for several layers; None if any is refused."""
+        out = []
+        for layer in layers:
+            t = self.write_target(session, layer, dst_start, n, row_shape, dtype, device)
+            if t is None:
+                return None
+            out.append(t)
+        return out
+
     def drop(self, session: str) -> None:
         self._sessions.pop(session, None)
 

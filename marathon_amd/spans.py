@@ -96,6 +96,18 @@ class CacheSet:
     def slots_of(self, t: torch.Tensor) -> int:
         return t.shape[0] * (1 if self.layout == "flat" else self.block_size)
 
+    def base_tables(self):
+        """``(k, v, caps)``: per-(group, layer) K and V base addresses (uint64) and
+        per-group slot capacities, computed once per CacheSet."""
+        got = getattr(self, "_bases", None)
+        if got is None:
+            eb = self.first.element_size()
+            k = np.array([[t.data_ptr() for t in row] for row in self.caches], dtype=np.uint64)
+            v = k + np.uint64(self.head_size * eb)
+            caps = np.array([self.slots_of(row[0]) for row in self.caches], dtype=np.int64)
+            got = self._bases = (k, v, caps)
+        return got
+
 
 class _Staging:
     """Host arrays bound for the device, packed into one pinned buffer and copied with
@@ -246,10 +258,7 @@ class ShiftPlan:
     def _side(cs: CacheSet, mode: str, index, stage: _Staging, place) -> dict:
         if mode not in MODES:
             raise ValueError(f"mode {mode!r}")
-        eb = cs.first.element_size()
-        k = np.array([[t.data_ptr() for t in row] for row in cs.caches], dtype=np.uint64)
-        v = k + np.uint64(cs.head_size * eb)
-        caps = np.array([cs.slots_of(row[0]) for row in cs.caches], dtype=np.int64)
+        k, v, caps = cs.base_tables()
         out = {
             "cs": cs,
             "mode": mode,
