@@ -53,7 +53,7 @@
 #define MKV_PASSES_4B 4
 #endif
 #ifndef MKV_PASSES_1B
-#define MKV_PASSES_1B 4
+#define MKV_PASSES_1B 2
 #endif
 
 // 1: store V before rotating K (frees its registers during the rotation).  Measured
@@ -64,7 +64,7 @@
 #endif
 
 #ifndef MKV_WG_THREADS
-#define MKV_WG_THREADS 256
+#define MKV_WG_THREADS 128
 #endif
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs; with
 // the remap, XCD k walks the k-th contiguous eighth of the tiles (smaller per-XCD set
@@ -75,8 +75,9 @@
 
 namespace {
 
-constexpr int kThreads = MKV_WG_THREADS;  // a multiple of the 64-lane wave
+constexpr int kThreads = MKV_WG_THREADS;  // shift kernel; a multiple of the 64-lane wave
 constexpr int kWaves = kThreads / 64;
+constexpr int kPlanThreads = 256;  // plan kernel
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Global-address-space view: keeps the compiler on global_load/global_store rather
@@ -426,20 +427,20 @@ __device__ __forceinline__ bool resolve(const DevSide& sd, int64_t cap, int64_t 
 // grid-stride share of the tokens into records and of (span, frequency) pairs into
 // the cos/sin tables.
 
-__global__ __launch_bounds__(kThreads) void plan_kernel(PlanParams p) {
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
   extern __shared__ int64_t s_pre[];  // [n_spans + 1]: exclusive prefix of tokens
-  __shared__ int64_t s_part[kThreads];
+  __shared__ int64_t s_part[kPlanThreads];
   const int tid = threadIdx.x;
   const int n = p.n_spans;
 
-  const int per = (n + kThreads - 1) / kThreads;
+  const int per = (n + kPlanThreads - 1) / kPlanThreads;
   const int b = tid * per;
   const int e = min(b + per, n);
   int64_t sum = 0;
   for (int i = b; i < e; ++i) sum += max(p.spans[i].n_tokens, 0);
   s_part[tid] = sum;
   __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
     const int64_t v = tid >= off ? s_part[tid - off] : 0;
     __syncthreads();
     s_part[tid] += v;
@@ -450,11 +451,11 @@ __global__ __launch_bounds__(kThreads) void plan_kernel(PlanParams p) {
     s_pre[i] = run;
     run += max(p.spans[i].n_tokens, 0);
   }
-  if (tid == kThreads - 1) s_pre[n] = s_part[kThreads - 1];
+  if (tid == kPlanThreads - 1) s_pre[n] = s_part[kPlanThreads - 1];
   __syncthreads();
   const int64_t actual = s_pre[n];
-  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kThreads + tid;
-  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kPlanThreads + tid;
+  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
 
   if (gtid == 0 && p.err != nullptr) {
     bool bad = actual > p.total_tokens;
@@ -1042,12 +1043,12 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
 
   const int64_t pairs = static_cast<int64_t>(d->n_spans) * (d->rotary / 2);
   const int64_t work = d->total_tokens > pairs ? d->total_tokens : pairs;
-  int64_t plan_grid = (work + kThreads - 1) / kThreads;
+  int64_t plan_grid = (work + kPlanThreads - 1) / kPlanThreads;
   if (plan_grid > 4096) plan_grid = 4096;
   if (plan_grid < 1) plan_grid = 1;
   const size_t lds = sizeof(int64_t) * (static_cast<size_t>(d->n_spans) + 1);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kThreads), lds,
+  hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kPlanThreads), lds,
                      st, pp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "plan launch failed: %s", hipGetErrorString(e));
