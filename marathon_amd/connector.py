@@ -97,6 +97,27 @@ class Load:
         return int(self.dst_start)
 
 
+class _CacheSets:
+    """CacheSets by role, rebuilt only when the tensors they describe change.
+
+    A CacheSet validates every tensor and reads every base address once; a step that
+    reuses the same caches should not pay that again.  The key is the tensors' ids:
+    the cached set keeps its tensors alive, so an id cannot be reused while cached.
+    """
+
+    def __init__(self, block_size: int) -> None:
+        self.block_size = block_size
+        self._sets: dict[str, tuple] = {}
+
+    def get(self, role: str, caches: list, layout: str, block_size: int | None = None) -> CacheSet:
+        key = tuple(tuple(id(t) for t in row) for row in caches)
+        hit = self._sets.get(role)
+        if hit is None or hit[0] != key:
+            bs = self.block_size if block_size is None else block_size
+            hit = self._sets[role] = (key, CacheSet([list(r) for r in caches], layout, bs))
+        return hit[1]
+
+
 def paged_index(items: list, block_size: int):
     """Address the paged side of a batch of loads or saves: ``(mode, index, rows)``.
 
@@ -169,7 +190,8 @@ def accept_multi(loads: list, num_computed: int, num_prompt_tokens: int, block_s
 
 
 class ShiftLoader:
-    """Loads reused spans from a :class:`ShiftStore` into registered paged caches."""
+    """Loads reused spans from a session store (the flat :class:`ShiftStore` or the
+    :class:`BlockShiftStore`) into registered paged caches."""
 
     def __init__(
         self,
@@ -189,6 +211,7 @@ class ShiftLoader:
         self.hnd: bool | None = None
         self.head_size: int | None = None
         self.last_plan: ShiftPlan | None = None
+        self._sets = _CacheSets(self.block_size)
 
     def register_kv_caches(self, kv_caches: dict) -> None:
         """Record the per-layer paged caches and their layout (:393-412)."""
@@ -196,9 +219,6 @@ class ShiftLoader:
         shape = next(iter(self._kv.values())).shape
         self.hnd = detect_hnd(shape, self.block_size)
         self.head_size = shape[3] // 2
-        self._dst = CacheSet([list(self._kv.values())], "hnd" if self.hnd else "nhd",
-                             self.block_size)
-        self._pool_set: tuple | None = None  # (pool ids, CacheSet) of a block store
         one = next(iter(self._kv.values()))
         if one.is_cuda:
             _lib.lib()  # the kernels are compiled ahead of time: only load the library
@@ -242,24 +262,21 @@ class ShiftLoader:
                 tab_off[sess] = off
                 tabs.append(t)
                 off += t.size
-            pools = [self.store.pool(name) for name in names]
-            key = tuple(id(p) for p in pools)
-            if self._pool_set is None or self._pool_set[0] != key:
-                self._pool_set = (key, CacheSet([pools], "nhd", self.store.block_size))
-            src = self._pool_set[1]
+            src = self._sets.get("store", [[self.store.pool(name) for name in names]], "nhd",
+                                 self.store.block_size)
             src_mode, src_index = "table", torch.from_numpy(np.concatenate(tabs))
             for load, (dpos, didx) in zip(taken, dst_rows):
                 rows.append((load.src_start, dpos, tab_off[load.session], didx, load.n,
                              int(load.delta), 0, 0))
         else:
-            src = CacheSet(
-                [[self.store.buffer(sess, name) for name in names] for sess in groups], "flat"
-            )
+            src = self._sets.get(
+                "store", [[self.store.buffer(sess, name) for name in names] for sess in groups],
+                "flat")
             src_mode, src_index = "flat", None
             for load, (dpos, didx) in zip(taken, dst_rows):
                 rows.append((load.src_start, dpos, 0, didx, load.n, int(load.delta),
                              groups[load.session], 0))
-        dst = self._dst
+        dst = self._sets.get("paged", [list(self._kv.values())], "hnd" if self.hnd else "nhd")
         k_scale = None
         if dst.first.dtype == torch.float8_e4m3fn:
             k_scale = torch.tensor([float(self.k_scales.get(name, 1.0)) for name in names])
@@ -311,15 +328,7 @@ class ShiftSaver:
         self.store = store
         self.block_size = int(block_size)
         self.last_plan: ShiftPlan | None = None
-        self._sets: dict[str, tuple] = {}  # role -> (tensor ids, CacheSet)
-
-    def _cached(self, role: str, tensors: list, layout: str) -> CacheSet:
-        """The CacheSet of ``tensors``, rebuilt only when the tensors change."""
-        key = tuple(id(t) for t in tensors)
-        hit = self._sets.get(role)
-        if hit is None or hit[0] != key:
-            hit = self._sets[role] = (key, CacheSet([list(tensors)], layout, self.block_size))
-        return hit[1]
+        self._sets = _CacheSets(self.block_size)
 
     def _plan(self, names: list, caches: list, saves: list) -> int:
         first = caches[0]
@@ -361,18 +370,19 @@ class ShiftSaver:
                 tab_off[sess] = off
                 tabs.append(t)
                 off += t.size
-            dst = self._cached("pools", [self.store.pool(name) for name in names], "nhd")
+            dst = self._sets.get("store", [[self.store.pool(name) for name in names]], "nhd",
+                                 self.store.block_size)
             dst_mode, dst_index = "table", torch.from_numpy(np.concatenate(tabs))
             for sv, (spos, sidx) in zip(taken, src_rows):
                 rows.append((spos, int(sv.dst_start), sidx, tab_off[sv.session], sv.n, 0, 0, 0))
         else:
-            dst = CacheSet(bufs, "flat")
+            dst = self._sets.get("store", bufs, "flat")
             dst_mode, dst_index = "flat", None
             for sv, (spos, sidx) in zip(taken, src_rows):
                 rows.append((spos, int(sv.dst_start), sidx, 0, sv.n, 0, 0, groups[sv.session]))
         plan = ShiftPlan(
             np.array(rows, dtype=_lib.SPAN_DTYPE),
-            self._cached("paged", caches, "hnd" if hnd else "nhd"),
+            self._sets.get("paged", [caches], "hnd" if hnd else "nhd"),
             dst,
             inv_freq=None,
             src_mode=src_mode,

@@ -230,17 +230,19 @@ def test_saver_matches_a_torch_gather(gpu):
                 assert torch.equal(got, want), (hnd, name, sv.session)
 
 
-def test_block_store_saver_and_loader_match_torch(gpu):
+@pytest.mark.parametrize("store_bs", [16, 32])
+def test_block_store_saver_and_loader_match_torch(gpu, store_bs):
     """Saves into the block store's pool (host slots and block tables), read back
-    through the store, then a load out of the pool: bytes equal a torch gather."""
+    through the store, then a load out of the pool: bytes equal a torch gather.  The
+    store's blocks need not be the paged cache's size."""
     g = torch.Generator(device=gpu)
     g.manual_seed(7)
     kv = {f"l{i}": torch.randn(64, H, BS, 2 * D, device=gpu, generator=g).to(torch.bfloat16)
           for i in range(3)}
-    store = BlockShiftStore(budget_tokens=4096, device=str(gpu), block_size=BS)
+    store = BlockShiftStore(budget_tokens=4096, device=str(gpu), block_size=store_bs)
     saver = ShiftSaver(store, BS)
     perm = torch.randperm(64).tolist()
-    print("case block store saves", flush=True)
+    print(f"case block store saves (store blocks of {store_bs})", flush=True)
     assert store.reserve("b", 0, 16)  # "b" holds [0, 16) already
     sa = Save("a", slots(perm[:20], 5, 5 + 300, BS), 0)
     sb = Save.from_blocks("b", perm[20:], 16, 16 + 200)
