@@ -303,7 +303,12 @@ class ShiftPlan:
 
     def launch(self, stream: int | None = None, error_flags: torch.Tensor | None = None) -> None:
         """Enqueue the shift on ``stream`` (default: current): a plan launch and a shift
-        launch per 4096 spans."""
+        launch per 4096 spans.
+
+        Nothing is allocated, copied or cleared here, so a launch can be captured into a
+        HIP graph and replayed.  The plan must be built before the capture begins and the
+        capture must start after its tables have arrived (``torch.cuda.graph`` begins
+        with a device synchronisation)."""
         if stream is None:
             stream = current_stream(self.device)
         L = _lib.lib()
@@ -311,7 +316,8 @@ class ShiftPlan:
             if int(stream) not in self._synced:
                 # the tables were copied on the stream current at build time
                 ext = torch.cuda.ExternalStream(int(stream), device=self.device)
-                ext.wait_event(self._ready)
+                if not torch.cuda.is_current_stream_capturing():
+                    ext.wait_event(self._ready)
                 for t in (*self._keep, self.workspace):
                     t.record_stream(ext)
                 self._synced.add(int(stream))

@@ -227,3 +227,35 @@ def test_single_span_out_of_range_slot_is_flagged_and_skipped(gpu):
     torch.cuda.synchronize(gpu)
     assert int(flags.item()) == _lib.MKV_FLAG_DST_RANGE
     assert torch.equal(kv.view(torch.int16), kv_ok.view(torch.int16))
+
+
+def test_plan_launch_replays_from_a_hip_graph(gpu):
+    """A captured launch replays exactly like an eager one: three replays, with eager
+    work between them (new source values, a cleared destination, an eager launch that
+    gives the expected bytes), each replay checked byte for byte."""
+    print("case graph capture of a batched plan", flush=True)
+    wl = W.config3(gpu, layers=2, history=1024, dst_fill="zeros")
+    plan = wl.plan()
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)  # warm-up, eager
+    torch.cuda.synchronize(gpu)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.launch(error_flags=flags)
+    for i in range(3):
+        for c in wl.src.caches[0]:
+            c.mul_(-1.0 if i % 2 == 0 else 0.5)  # exact in bf16: a sign flip, a halving
+        for c in wl.dst.caches[0]:
+            c.zero_()
+        plan.launch(error_flags=flags)
+        torch.cuda.synchronize(gpu)
+        want = [c.clone() for c in wl.dst.caches[0]]
+        for c in wl.dst.caches[0]:
+            c.zero_()
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        for layer, (a, b) in enumerate(zip(wl.dst.caches[0], want)):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (i, layer)
+        assert bool(want[0].view(torch.int16).any())
+    assert int(flags.item()) == 0
