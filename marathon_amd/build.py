@@ -3,6 +3,8 @@
 ``python -m marathon_amd.build`` (or ``__graft_entry__.build()``) compiles
 ``csrc/kvshift.hip`` into ``_lib/libmarathon_kvshift.so`` with hipcc.  It always
 recompiles: the build is a few seconds and a stale library is worse than a slow one.
+:func:`build_test_libraries` compiles the GPU tests' own HIP helpers (``tests/hip``)
+into ``tests/_lib`` with the same flags.
 """
 
 from __future__ import annotations
@@ -18,6 +20,8 @@ SRC = os.path.join(HERE, "csrc", "kvshift.hip")
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 OUT = os.path.join(OUT_DIR, "libmarathon_kvshift.so")
+TEST_SRC_DIR = os.path.join(ROOT, "tests", "hip")
+TEST_OUT_DIR = os.path.join(ROOT, "tests", "_lib")
 
 ARCH = "gfx950"
 
@@ -48,10 +52,11 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
 
 
-def build_library(verbose: bool = False) -> str:
-    os.makedirs(OUT_DIR, exist_ok=True)
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", SRC, "-o", tmp]
+def _compile(src: str, out: str, verbose: bool) -> str:
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{os.path.join(HERE, 'csrc')}", src,
+           "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -62,9 +67,27 @@ def build_library(verbose: bool = False) -> str:
         raise RuntimeError("hipcc failed:\n" + "\n".join(noise))
     if verbose and noise:
         print("\n".join(noise), file=sys.stderr)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
+
+
+def build_library(verbose: bool = False) -> str:
+    return _compile(SRC, OUT, verbose)
+
+
+def build_test_libraries(verbose: bool = False) -> list:
+    """``tests/hip/<name>.hip`` -> ``tests/_lib/lib<name>.so`` (test helpers only)."""
+    if not os.path.isdir(TEST_SRC_DIR):
+        return []
+    outs = []
+    for fn in sorted(os.listdir(TEST_SRC_DIR)):
+        if fn.endswith(".hip"):
+            out = os.path.join(TEST_OUT_DIR, f"lib{fn[:-4]}.so")
+            outs.append(_compile(os.path.join(TEST_SRC_DIR, fn), out, verbose))
+    return outs
 
 
 if __name__ == "__main__":
     print(build_library(verbose=True))
+    for path in build_test_libraries(verbose=True):
+        print(path)

@@ -1,0 +1,62 @@
+// fp8 e4m3fn (OCP) codec for gfx950 device code: decode, requantise, encode.
+//
+// Shared by the shift kernel and the test library that checks it value by value.
+// gfx950's v_cvt_pk_f32_fp8 decodes every code exactly; v_cvt_pk_fp8_f32 rounds to
+// nearest even, and its NaN code is 0xFF where the format's canonical NaN is 0x7F, so
+// callers rewrite NaN lanes to 0x7F.
+//
+// quant(): y / scale through Markstein's correction, q0 = RN(y * r),
+// q = fma(fma(-q0, scale, y), r, q0) with r = RN(1 / scale).  It equals the correctly
+// rounded quotient for every fp32 y with 2^-12 <= |y / scale| < 2^10 at scales in
+// [0.01, 0.1] (checked exhaustively on the CPU); smaller quotients encode to a signed
+// zero either way, larger ones cannot occur.  copysign keeps -0 / scale = -0.  The
+// result is clamped to +-448 with IEEE minNum/maxNum, which turn a NaN into 448: callers
+// that can see NaN inputs rewrite those bytes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mkv_fp8 {
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+// Whether any byte of w is a NaN code (S.1111.111).
+__device__ __forceinline__ bool has_nan_code(uint32_t w) {
+  return (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0;
+}
+
+// The four codes of w, low byte first, as exact floats.
+__device__ __forceinline__ void decode4(uint32_t w, float* out) {
+  const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  out[0] = lo[0];
+  out[1] = lo[1];
+  out[2] = hi[0];
+  out[3] = hi[1];
+}
+
+__device__ __forceinline__ float clamp448(float q) {
+  return __builtin_fmaxf(__builtin_fminf(q, 448.0f), -448.0f);
+}
+
+// clamp(RN(y / scale)); rcp must be RN(1 / scale).
+__device__ __forceinline__ float quant(float y, float scale, float rcp) {
+  const float q0 = y * rcp;
+  const float r = __builtin_fmaf(-q0, scale, y);
+  return clamp448(__builtin_copysignf(__builtin_fmaf(r, rcp, q0), y));
+}
+
+// Four in-range floats to four codes (round to nearest even), low byte first.
+__device__ __forceinline__ uint32_t encode4(const float* q) {
+  int v = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  v = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], v, true);
+  return static_cast<uint32_t>(v);
+}
+
+// Byte b of w set to the canonical NaN code.
+__device__ __forceinline__ uint32_t with_nan(uint32_t w, int b) {
+  return (w & ~(0xFFu << (8 * b))) | (0x7Fu << (8 * b));
+}
+
+}  // namespace mkv_fp8

@@ -35,6 +35,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "fp8_e4m3.h"
 #include "marathon_kvshift.h"
 
 #pragma clang fp contract(off)
@@ -311,41 +312,14 @@ struct Rotor<MKV_F32> {
   }
 };
 
-// fp8 e4m3fn, using gfx950's OCP conversions: v_cvt_pk_f32_fp8 decodes every code
-// exactly, v_cvt_pk_fp8_f32 rounds to nearest even (both checked against the format
-// definition over all codes, all ties and near-ties); its NaN code is 0xFF, so a lane
-// whose inputs hold a NaN code rewrites those bytes to 0x7F.  y / scale uses Markstein's
-// correction, q0 = RN(y * r), q = fma(fma(-q0, scale, y), r, q0) with r = RN(1 / scale),
-// which equals the correctly rounded quotient (checked for every fp32 y with
-// 2^-12 <= |y / scale| < 2^10 at 21 scales in [0.01, 0.1]; smaller quotients encode to
-// a signed zero either way, larger ones cannot occur); copysign keeps -0 / scale = -0.
-typedef float f2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ bool has_nan_code(uint32_t w) {
-  // a byte whose low 7 bits are all ones (S.1111.111) is NaN
-  return (((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u) != 0;
-}
-
+// fp8 e4m3fn: dequantise with the layer's K scale, rotate as above, requantise
+// (codec in fp8_e4m3.h).  Lanes whose inputs hold a NaN code recompute which outputs
+// are NaN and write the canonical 0x7F there.
 template <>
 struct Rotor<MKV_FP8_E4M3> {
-  // y / scale, correctly rounded, clamped to the format's range.  A NaN comes out as
-  // 448 here (IEEE minNum/maxNum return the other operand); run() rewrites it.
-  static __device__ __forceinline__ float quant(float y, float scale, float rcp) {
-    const float q0 = y * rcp;
-    const float r = __builtin_fmaf(-q0, scale, y);
-    const float q = __builtin_copysignf(__builtin_fmaf(r, rcp, q0), y);
-    return __builtin_fmaxf(__builtin_fminf(q, 448.0f), -448.0f);
-  }
-  static __device__ __forceinline__ void decode4(uint32_t w, float* out) {
-    const f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-    const f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
-    out[0] = lo[0];
-    out[1] = lo[1];
-    out[2] = hi[0];
-    out[3] = hi[1];
-  }
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
                                               const float* s, float scale, float rcp) {
+    using namespace mkv_fp8;
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -357,9 +331,7 @@ struct Rotor<MKV_FP8_E4M3> {
         const int e = 4 * w + b;
         q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale, rcp);
       }
-      int v = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-      v = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], v, true);
-      out[w] = static_cast<uint32_t>(v);
+      out[w] = encode4(q);
     }
     const bool any_nan = has_nan_code(mine[0]) | has_nan_code(mine[1]) | has_nan_code(mine[2]) |
                          has_nan_code(mine[3]) | has_nan_code(part[0]) | has_nan_code(part[1]) |
@@ -375,7 +347,7 @@ struct Rotor<MKV_FP8_E4M3> {
         for (int b = 0; b < 4; ++b) {
           const int e = 4 * w + b;
           const float y = rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]);
-          if (y != y) out[w] = (out[w] & ~(0xFFu << (8 * b))) | (0x7Fu << (8 * b));
+          if (y != y) out[w] = with_nan(out[w], b);
         }
       }
     }
