@@ -75,15 +75,42 @@ def build_library(verbose: bool = False) -> str:
     return _compile(SRC, OUT, verbose)
 
 
+def _compile_c_host(src: str, out: str, verbose: bool) -> str:
+    """A C host program against the library's C ABI and the HIP runtime, built by gcc
+    (no HIP compiler involved: this is what an outside C caller does)."""
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    rocm = os.path.dirname(os.path.dirname(os.path.realpath(hipcc())))
+    rel = os.path.relpath(OUT_DIR, os.path.dirname(out))
+    cmd = ["gcc", "-std=c11", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           f"-I{os.path.join(rocm, 'include')}", f"-I{INCLUDE}", src, f"-L{OUT_DIR}",
+           "-lmarathon_kvshift", f"-L{os.path.join(rocm, 'lib')}", "-lamdhip64", "-lm",
+           f"-Wl,-rpath,$ORIGIN/{rel}", f"-Wl,-rpath,{os.path.join(rocm, 'lib')}",
+           "-o", out + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("gcc failed:\n" + res.stderr)
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_test_libraries(verbose: bool = False) -> list:
-    """``tests/hip/<name>.hip`` -> ``tests/_lib/lib<name>.so`` (test helpers only)."""
-    if not os.path.isdir(TEST_SRC_DIR):
-        return []
+    """The GPU tests' own native helpers (test infrastructure only):
+    ``tests/hip/<name>.hip`` -> ``tests/_lib/lib<name>.so`` and
+    ``tests/c/<name>.c`` -> ``tests/_lib/<name>`` (C programs on the C ABI)."""
     outs = []
-    for fn in sorted(os.listdir(TEST_SRC_DIR)):
-        if fn.endswith(".hip"):
-            out = os.path.join(TEST_OUT_DIR, f"lib{fn[:-4]}.so")
-            outs.append(_compile(os.path.join(TEST_SRC_DIR, fn), out, verbose))
+    if os.path.isdir(TEST_SRC_DIR):
+        for fn in sorted(os.listdir(TEST_SRC_DIR)):
+            if fn.endswith(".hip"):
+                out = os.path.join(TEST_OUT_DIR, f"lib{fn[:-4]}.so")
+                outs.append(_compile(os.path.join(TEST_SRC_DIR, fn), out, verbose))
+    c_dir = os.path.join(ROOT, "tests", "c")
+    if os.path.isdir(c_dir):
+        for fn in sorted(os.listdir(c_dir)):
+            if fn.endswith(".c"):
+                out = os.path.join(TEST_OUT_DIR, fn[:-2])
+                outs.append(_compile_c_host(os.path.join(c_dir, fn), out, verbose))
     return outs
 
 
