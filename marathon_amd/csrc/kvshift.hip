@@ -504,9 +504,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
 
 // -------------------------------------------------------------------- shift kernel
 //
-// Grid (token tiles, layers).  Wave w of the workgroup runs passes q = w + 4u
+// Grid (token tiles, layers).  Wave w of the workgroup runs passes q = w + kWaves * u
 // (u < U); pass q covers rows [q * rpw, (q + 1) * rpw) of the tile's token-major
-// (token, head) rows.  UNIFORM: heads % rpw == 0, so a pass is one token.
+// (token, head) rows.  UNIFORM: heads % rpw == 0, so every row of a pass belongs to
+// one token.
 
 template <int DT, bool BATCHED, bool UNIFORM>
 __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
