@@ -259,3 +259,32 @@ def test_plan_launch_replays_from_a_hip_graph(gpu):
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (i, layer)
         assert bool(want[0].view(torch.int16).any())
     assert int(flags.item()) == 0
+
+
+def test_connector_loader_fp8_with_layer_scales(gpu):
+    """The loader on an fp8 paged cache: each layer's K scale reaches the kernel, K is
+    dequantised, rotated and requantised exactly as the oracle's fp8 rule, V is copied."""
+    print("case connector loader fp8", flush=True)
+    layers, heads, d, bs = 3, 8, 128, 16
+    names = [f"layers.{i}" for i in range(layers)]
+    scales = {name: s for name, s in zip(names, (0.013, 0.05, 0.094))}
+    store = ShiftStore(budget_tokens=4096, device=str(gpu), slab=512)
+    g = torch.Generator().manual_seed(33)
+    assert store.reserve("s", 0, 400)
+    for name in names:
+        x = (torch.randn(400, heads, 2 * d, generator=g) / scales[name]).clamp(-448, 448)
+        store.write("s", name, 0, x.to(torch.float8_e4m3fn).to(gpu))
+    kv = {name: torch.zeros(40, heads, bs, 2 * d, dtype=torch.float8_e4m3fn, device=gpu)
+          for name in names}
+    loader = ShiftLoader(store, bs, inv_freq(), k_scales=scales)
+    loader.register_kv_caches(kv)
+    perm = torch.randperm(40, generator=g).tolist()
+    ld = Load("s", slots(perm, 21, 21 + 333, bs), src_start=50, delta=-29)
+    assert loader.start_load_kv([ld]) == 333 * layers
+    torch.cuda.synchronize(gpu)
+    for name in names:
+        want = np.zeros_like(bits(kv[name]))
+        src_rows = bits(store.read("s", name, 50, 333))
+        orc.scatter_shifted(src_rows, want, ld.slots.numpy(), bs, True, -29,
+                            inv_freq().numpy(), "fp8", np.float32(scales[name]))
+        assert np.array_equal(bits(kv[name]), want), name
