@@ -94,15 +94,15 @@ def spot_check(wl, rows: int = 96, seed: int = 0) -> int:
 
 
 def cpu_baseline(reps: int = 3) -> dict:
-    """The reference torch path on the host CPU, config 1 (28 layers x 4,096 tokens)."""
+    """The reference torch path on the host CPU: Qwen3-0.6B shape, 28 layers x 4,096 tokens."""
     import platform
 
     import torch
 
-    from marathon_amd.workloads import config1_cpu
+    from marathon_amd.workloads import qwen3_0_6b_cpu_shift
     from oracle import torch_path
 
-    cfg = config1_cpu()
+    cfg = qwen3_0_6b_cpu_shift()
     emb = torch_path.rope_emb_tables(cfg["delta"], cfg["inv_freq"])
     n = cfg["src"][0].shape[0]
     layers = len(cfg["src"])
@@ -173,17 +173,17 @@ def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
-def other_configs(dev, steps: int, warmup: int, stream) -> dict:
-    """Informational: the other GPU configurations, one launch per step each."""
+def other_workloads(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: the other GPU workloads, one launch per step each."""
     import numpy as np
     import torch
 
     from marathon_amd import workloads as W
 
     out = {}
-    for name, make in (("config2_qwen3_8b_single_span_bf16", lambda: W.config2(dev)),
-                       ("config4_qwen3_14b_multispan_fp8", lambda: W.config4(dev)),
-                       ("config5_32_sessions_batched_bf16", lambda: W.config5(dev))):
+    for name, make in (("qwen3_8b_single_span_bf16", lambda: W.qwen3_8b_single_span(dev)),
+                       ("qwen3_14b_multispan_fp8", lambda: W.qwen3_14b_multispan_fp8(dev)),
+                       ("batched_32_sessions_bf16", lambda: W.batched_sessions(dev))):
         log(f"timing {name}")
         wl = make()
         plan = wl.plan()
@@ -207,9 +207,10 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
     slot lists) into an HND paged cache.  Times the whole call from Python (store
     checks, span table, one pinned upload, plan + shift kernels) to the stream's
-    completion, next to the kernels alone on the same plan.  Two steps: config 3's eight
-    spans, and one 29,232-token load, the size of the reference's in-engine measurement
-    (docs/findings.md:664-666: 34.4 ms copy_ms, 6.2 ms of it the kernel)."""
+    completion, next to the kernels alone on the same plan.  Two steps: the Qwen3-14B
+    multi-span workload's eight spans, and one 29,232-token load, the size of the
+    reference's in-engine measurement (docs/findings.md:664-666: 34.4 ms copy_ms,
+    6.2 ms of it the kernel)."""
     import numpy as np
     import torch
 
@@ -219,7 +220,7 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     from marathon_amd.shift_kernels import inv_freq_for
 
     layers, heads, d, bs = 40, 8, 128, 16
-    lay = W.config3_layout()
+    lay = W.qwen3_14b_multispan_layout()
     history = lay.src_history
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
@@ -236,7 +237,7 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     loader = ShiftLoader(store, bs, inv_freq_for(d, 1e6))
     loader.register_kv_caches(kv)
     cases = {
-        "config3_8_spans": lambda: [
+        "qwen3_14b_8_spans": lambda: [
             Load.from_blocks("s", table, int(dst), int(dst) + int(n), int(dl))
             for dst, n, dl in zip(lay.dst_start, lay.length, lay.delta)],
         "one_load_29232_tokens": lambda: [Load.from_blocks("s", table, 0, 29232, -186)],
@@ -336,8 +337,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-shape", action="store_true")
-    ap.add_argument("--no-other-configs", action="store_true",
-                    help="skip the informational timings of configs 2, 4 and 5")
+    ap.add_argument("--no-other-workloads", "--no-other-configs", dest="no_other_workloads",
+                    action="store_true",
+                    help="skip the informational timings of the Qwen3-8B single-span, fp8 "
+                    "multi-span and batched-session workloads")
     ap.add_argument("--no-connector-step", action="store_true",
                     help="skip the end-to-end connector load and save step timings")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -347,7 +350,7 @@ def main() -> int:
         print(
             "bench.py measures one GPU: the shift needs no collective and this build runs on "
             "a single MI355X (per-rank sharding is by KV head / layer / session with no "
-            "exchange; see DESIGN.md).  Run with --gpus 1.",
+            "exchange).  Run with --gpus 1.",
             file=sys.stderr,
         )
         return 2
@@ -360,8 +363,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
-    log("building config 3 workload (40 layers, 30,720-token history, 8 spans)")
-    wl = W.config3(dev)
+    log("building the Qwen3-14B multi-span workload (40 layers, 30,720-token history, 8 spans)")
+    wl = W.qwen3_14b_multispan(dev)
     plan = wl.plan()
     torch.cuda.synchronize()
     log(f"spans={len(wl.spans)} tokens={wl.tokens} bytes={plan.algorithmic_bytes}")
@@ -396,8 +399,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         log("reference benchmark shape (30,720 x 40, delta 186)")
         extra["reference_shape"] = reference_shape(dev, max(5, args.steps // 2), args.warmup, stream)
-    if not args.no_other_configs:
-        extra["other_configs"] = other_configs(dev, max(5, args.steps // 2), args.warmup, stream)
+    if not args.no_other_workloads:
+        extra["other_workloads"] = other_workloads(dev, max(5, args.steps // 2), args.warmup,
+                                                   stream)
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
         extra["connector_step"] = connector_step(dev, max(5, args.steps), args.warmup)
@@ -405,7 +409,7 @@ def main() -> int:
         extra["save_step"] = save_step(dev, max(5, args.steps), args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
-        log("cpu baseline (reference torch path on the host, config 1)")
+        log("cpu baseline (reference torch path on the host, Qwen3-0.6B shape)")
         cpu = cpu_baseline()
 
     tokens = int(bytes_step // (2 * 40 * 8 * 256 * 2))

@@ -1,4 +1,4 @@
-"""Seeded synthetic shift workloads: the five benchmark configurations.
+"""Seeded synthetic shift workloads: the benchmark and parity workloads.
 
 Shared geometry (Qwen3 KV): 8 KV heads, head_dim 128, full NeoX rotary, theta 1e6,
 block_size 16.  Synthetic data (there is no checkpoint to load): K/V ~ N(0, 1) drawn
@@ -11,13 +11,14 @@ on the device from seeded generators.
 3. Qwen3-14B-shaped multi-span: 40 layers, history 30,720, 8 spans of 256..8192
    tokens, deltas in [-2048, 2048] of both signs and one 0, no span boundary on a
    multiple of 16, disjoint and order-preserving, shuffled block tables.
-4. Config 3's layout in fp8 e4m3fn with per-layer fp32 scales in [0.01, 0.1].
+4. The Qwen3-14B multi-span layout in fp8 e4m3fn with per-layer fp32 scales in
+   [0.01, 0.1].
 5. 32 sessions x 36 layers, histories in [2048, 32768], 1..6 spans per session,
    deltas in [-4096, 4096], one span table, one shared paged destination.
 
 The source is the session store in block layout (NHD blocks, read through a block
 table); the destination is an HND paged cache written through a slot mapping
-(configs 2-4) or through per-request block tables (config 5).
+(workloads 2-4) or through per-request block tables (workload 5).
 """
 
 from __future__ import annotations
@@ -119,7 +120,7 @@ def multispan_layout(
     raise RuntimeError("no span layout found; constraints too tight")
 
 
-def config3_layout(seed: int = 3, history: int = 30720) -> SpanLayout:
+def qwen3_14b_multispan_layout(seed: int = 3, history: int = 30720) -> SpanLayout:
     rng = np.random.default_rng(seed)
     lo, hi = (256, 8192) if history >= 30720 else (max(17, history // 120), max(33, history // 4))
     return multispan_layout(rng, history, 8, lo, hi, -2048, 2048, need_zero=True,
@@ -198,7 +199,7 @@ def single_session_workload(
     dst_fill: str = "zeros",
 ) -> Workload:
     """One session's store (NHD blocks via a shuffled table) -> one HND paged cache via
-    a slot mapping.  Configs 2-4."""
+    a slot mapping: the single-span and multi-span workloads, bf16 or fp8."""
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -248,25 +249,25 @@ def single_session_workload(
     )
 
 
-def config2(device, layers: int = 36, history: int = 16384, seed: int = 2, **kw) -> Workload:
+def qwen3_8b_single_span(device, layers: int = 36, history: int = 16384, seed: int = 2, **kw) -> Workload:
     cut = 512 * history // 16384
     lay = SpanLayout(np.array([cut]), np.array([0]), np.array([history - cut]),
                      np.array([-cut]), history, history - cut)
     return single_session_workload("qwen3-8b single span", lay, layers, device, seed=seed, **kw)
 
 
-def config3(device, layers: int = 40, history: int = 30720, seed: int = 3, **kw) -> Workload:
-    lay = config3_layout(seed, history)
+def qwen3_14b_multispan(device, layers: int = 40, history: int = 30720, seed: int = 3, **kw) -> Workload:
+    lay = qwen3_14b_multispan_layout(seed, history)
     return single_session_workload("qwen3-14b multi-span", lay, layers, device, seed=seed, **kw)
 
 
-def config4(device, layers: int = 40, history: int = 30720, **kw) -> Workload:
-    lay = config3_layout(3, history)
+def qwen3_14b_multispan_fp8(device, layers: int = 40, history: int = 30720, **kw) -> Workload:
+    lay = qwen3_14b_multispan_layout(3, history)
     return single_session_workload("qwen3-14b multi-span fp8", lay, layers, device, seed=4,
                                    dtype=torch.float8_e4m3fn, scale_seed=4, **kw)
 
 
-def config5_layouts(seed: int = 5, sessions: int = 32, hist_lo: int = 2048,
+def batched_sessions_layouts(seed: int = 5, sessions: int = 32, hist_lo: int = 2048,
                     hist_hi: int = 32768) -> list:
     rng = np.random.default_rng(seed)
     out = []
@@ -280,11 +281,11 @@ def config5_layouts(seed: int = 5, sessions: int = 32, hist_lo: int = 2048,
     return out
 
 
-def config5(device, layers: int = 36, seed: int = 5, sessions: int = 32, hist_lo: int = 2048,
+def batched_sessions(device, layers: int = 36, seed: int = 5, sessions: int = 32, hist_lo: int = 2048,
             hist_hi: int = 32768, dtype=torch.bfloat16) -> Workload:
     """32 sessions, each its own store (group), one shared HND destination pool; both
     sides addressed through block tables, so the slot math runs on the device."""
-    lays = config5_layouts(seed, sessions, hist_lo, hist_hi)
+    lays = batched_sessions_layouts(seed, sessions, hist_lo, hist_hi)
     rng = np.random.default_rng(seed + 1000)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -319,10 +320,10 @@ def config5(device, layers: int = 36, seed: int = 5, sessions: int = 32, hist_lo
     )
 
 
-# -------------------------------------------------------------------- CPU config 1
+# ------------------------------------------------------ the CPU reference workload
 
 
-def config1_cpu(layers: int = 28, n: int = 4096, delta: int = 37, seed: int = 1):
+def qwen3_0_6b_cpu_shift(layers: int = 28, n: int = 4096, delta: int = 37, seed: int = 1):
     """Flat store rows per layer and an HND paged cache per layer, on the CPU."""
     gen = torch.Generator().manual_seed(seed)
     src = [torch.randn(n, HEADS, 2 * HEAD_SIZE, dtype=torch.bfloat16, generator=gen)

@@ -103,34 +103,34 @@ def _check_full(wl, dtype_name, samples=192, seed=0, snapshot=True):
         assert np.array_equal(got[..., :D], want), f"K differs: span {sp} token {i} layer {layer}"
 
 
-def test_config2_full_size(gpu):
-    print("case config 2 full size (36 layers, 15,872 tokens)", flush=True)
-    wl = W.config2(gpu, dst_fill="random")
+def test_qwen3_8b_single_span_full_size(gpu):
+    print("case Qwen3-8B single span full size (36 layers, 15,872 tokens)", flush=True)
+    wl = W.qwen3_8b_single_span(gpu, dst_fill="random")
     _check_full(wl, "bf16")
     del wl
     torch.cuda.empty_cache()
 
 
-def test_config3_full_size(gpu):
-    print("case config 3 full size (40 layers, 8 spans)", flush=True)
-    wl = W.config3(gpu, dst_fill="random")
+def test_qwen3_14b_multispan_full_size(gpu):
+    print("case Qwen3-14B multi-span full size (40 layers, 8 spans)", flush=True)
+    wl = W.qwen3_14b_multispan(gpu, dst_fill="random")
     assert wl.tokens > 20000 and len(wl.spans) == 8
     _check_full(wl, "bf16")
     del wl
     torch.cuda.empty_cache()
 
 
-def test_config4_fp8_full_size(gpu):
-    print("case config 4 full size fp8", flush=True)
-    wl = W.config4(gpu)
+def test_qwen3_14b_multispan_fp8_full_size(gpu):
+    print("case Qwen3-14B multi-span fp8 full size", flush=True)
+    wl = W.qwen3_14b_multispan_fp8(gpu)
     _check_full(wl, "fp8")
     del wl
     torch.cuda.empty_cache()
 
 
-def test_config5_batched_full_size(gpu):
-    print("case config 5 full size (32 sessions x 36 layers)", flush=True)
-    wl = W.config5(gpu)
+def test_batched_sessions_full_size(gpu):
+    print("case batched sessions full size (32 sessions x 36 layers)", flush=True)
+    wl = W.batched_sessions(gpu)
     assert wl.src.groups == 32 and len(wl.spans) > 32
     _check_full(wl, "bf16", samples=128, snapshot=False)
     del wl
@@ -140,8 +140,8 @@ def test_config5_batched_full_size(gpu):
 def test_round_trip_at_full_size(gpu):
     """Shift by delta, then back by -delta: K returns within the double-rounding bound,
     V exactly."""
-    print("case round trip (config 3 layout, 40 layers)", flush=True)
-    wl = W.config3(gpu)
+    print("case round trip (Qwen3-14B multi-span layout, 40 layers)", flush=True)
+    wl = W.qwen3_14b_multispan(gpu)
     wl.plan().launch()
     back = [torch.zeros_like(c) for c in wl.src.caches[0]]
     # the way back: read the destination cache through the same slots, write a fresh
@@ -173,7 +173,7 @@ def test_fresh_rope_bar(gpu):
     """Keys RoPE'd at p (bf16), shifted by delta, against the same keys RoPE'd at p + delta
     in float64: max-abs <= 2e-2 where |k| < 4, and the double-rounding bound elsewhere."""
     print("case fresh RoPE (8 spans, 2 layers)", flush=True)
-    lay = W.config3_layout()
+    lay = W.qwen3_14b_multispan_layout()
     inv = W.inv_freq_for(D, 1e6)
     heads = 8
     g = torch.Generator(device=gpu)

@@ -1,7 +1,7 @@
 """Batched shifts on the GPU (one launch over a span table) against the oracle.
 
-Reduced-size versions of the multi-span (config 3), fp8 (config 4) and batched-session
-(config 5) workloads, every byte of every destination cache compared with the oracle's
+Reduced-size versions of the Qwen3-14B multi-span, its fp8 variant and the batched
+session workloads, every byte of every destination cache compared with the oracle's
 ``shift_spans``; and the connector-shaped loader reading straight out of a store.
 """
 
@@ -42,7 +42,7 @@ def _check_workload(wl, dev, dtype_name="bf16"):
 @pytest.mark.parametrize("history,layers", [(2048, 3), (4099, 2)])
 def test_multispan_matches_oracle(gpu, history, layers):
     print(f"case multispan history={history} layers={layers}", flush=True)
-    wl = W.config3(gpu, layers=layers, history=history, dst_fill="random")
+    wl = W.qwen3_14b_multispan(gpu, layers=layers, history=history, dst_fill="random")
     lay = wl.meta["layout"]
     assert np.any(lay.delta == 0) and np.any(lay.delta > 0) and np.any(lay.delta < 0)
     _check_workload(wl, gpu)
@@ -50,13 +50,13 @@ def test_multispan_matches_oracle(gpu, history, layers):
 
 def test_fp8_multispan_matches_oracle(gpu):
     print("case fp8 multispan", flush=True)
-    wl = W.config4(gpu, layers=3, history=2048)
+    wl = W.qwen3_14b_multispan_fp8(gpu, layers=3, history=2048)
     _check_workload(wl, gpu, "fp8")
 
 
 def test_batched_sessions_match_oracle(gpu):
     print("case batched sessions", flush=True)
-    wl = W.config5(gpu, layers=2, sessions=6, hist_lo=64, hist_hi=700)
+    wl = W.batched_sessions(gpu, layers=2, sessions=6, hist_lo=64, hist_hi=700)
     assert wl.src.groups == 6
     _check_workload(wl, gpu)
 
@@ -234,7 +234,7 @@ def test_plan_launch_replays_from_a_hip_graph(gpu):
     work between them (new source values, a cleared destination, an eager launch that
     gives the expected bytes), each replay checked byte for byte."""
     print("case graph capture of a batched plan", flush=True)
-    wl = W.config3(gpu, layers=2, history=1024, dst_fill="zeros")
+    wl = W.qwen3_14b_multispan(gpu, layers=2, history=1024, dst_fill="zeros")
     plan = wl.plan()
     flags = torch.zeros(1, dtype=torch.int32, device=gpu)
     plan.launch(error_flags=flags)  # warm-up, eager
