@@ -365,6 +365,29 @@ def save_step(dev, steps: int, warmup: int) -> dict:
             "kernel_ms": round(kms, 4),
             "kernel_GB_s": round(plan.algorithmic_bytes / (kms / 1e3) / 1e9, 1),
         }
+    # vLLM's per-layer hook for a decode step: 40 save_kv_layer calls, each its own
+    # launch (as the reference saves), or deferred to one launch in wait_for_save
+    for case, deferred in (("decode_step_40_layer_hooks", False),
+                           ("decode_step_40_layer_hooks_deferred", True)):
+        hook = ShiftSaver(store, bs, deferred=deferred)
+
+        def one_step():
+            saves = [Save.from_blocks("s", table, n - 1, n)]
+            for name in names:
+                hook.save_kv_layer(name, kv[name], saves)
+            hook.wait_for_save()
+
+        for _ in range(warmup):
+            one_step()
+        torch.cuda.synchronize()
+        e2e = []
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            one_step()
+            torch.cuda.synchronize()
+            e2e.append((time.perf_counter() - t0) * 1e3)
+        out[case] = {"tokens": 1, "ms_end_to_end": round(float(np.median(e2e)), 4)}
     del store, kv, saver
     torch.cuda.empty_cache()
     return out

@@ -324,11 +324,14 @@ class ShiftSaver:
     session's block table, so a save never reallocates and never copies what is stored.
     """
 
-    def __init__(self, store: ShiftStore | BlockShiftStore, block_size: int):
+    def __init__(self, store: ShiftStore | BlockShiftStore, block_size: int, *,
+                 deferred: bool = False):
         self.store = store
         self.block_size = int(block_size)
+        self.deferred = bool(deferred)
         self.last_plan: ShiftPlan | None = None
         self._sets = _CacheSets(self.block_size)
+        self._pending: list = []  # deferred: (layer name, paged cache, the step's saves)
 
     def _plan(self, names: list, caches: list, saves: list) -> int:
         first = caches[0]
@@ -395,8 +398,28 @@ class ShiftSaver:
         return sum(sv.n for sv in taken) * len(names)
 
     def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, saves: list) -> int:
-        """One layer, every save of the step (the reference's per-layer hook)."""
+        """One layer, every save of the step (the reference's per-layer hook).
+
+        Deferred (``deferred=True``): the layer is only recorded, and returns 0; the
+        step's :meth:`wait_for_save` saves every recorded layer in one launch.  vLLM
+        calls that hook at the end of the forward pass, when every layer's KV for the
+        step is final, and the store ends the step in the state per-layer saves leave.
+        """
+        if self.deferred:
+            self._pending.append((layer_name, kv_layer, saves))
+            return 0
         return self._plan([layer_name], [kv_layer], saves)
+
+    def wait_for_save(self) -> int:
+        """Flush the deferred layers: one launch per distinct list of saves (a step has
+        one).  Returns the token-layers saved; 0 when nothing is pending."""
+        pending, self._pending = self._pending, []
+        groups: dict[int, tuple] = {}
+        for name, cache, saves in pending:
+            names, caches, _ = groups.setdefault(id(saves), ([], [], saves))
+            names.append(name)
+            caches.append(cache)
+        return sum(self._plan(names, caches, saves) for names, caches, saves in groups.values())
 
     def save_all(self, kv_caches: dict, saves: list) -> int:
         """Every layer and every save of the step in one launch (at the end of a step)."""

@@ -277,3 +277,27 @@ def test_block_store_saver_and_loader_match_torch(gpu, store_bs):
             pair = torch.maximum(k0.abs(), torch.roll(k0, D // 2, -1).abs())
             assert bool(((got[..., :D].to(torch.float64) - ref).abs()
                          <= 2.0**-8 * (ref.abs() + 2 * pair) + 1e-6).all())
+
+
+def test_deferred_per_layer_saves_equal_one_save_all(gpu):
+    """vLLM's per-layer hook, deferred: save_kv_layer records, wait_for_save launches
+    once; the store ends with the same bytes and the same counters as save_all."""
+    print("case deferred per-layer saves", flush=True)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    kv = {f"l{i}": torch.randn(48, H, BS, 2 * D, device=gpu, generator=g).to(torch.bfloat16)
+          for i in range(4)}
+    table = torch.randperm(48).tolist()
+    stores = [BlockShiftStore(budget_tokens=4096, device=str(gpu), block_size=BS) for _ in range(2)]
+    eager = ShiftSaver(stores[0], BS)
+    deferred = ShiftSaver(stores[1], BS, deferred=True)
+    saves = [Save.from_blocks("s", table, 0, 500)]
+    assert eager.save_all(kv, saves) == 500 * 4
+    for name, cache in kv.items():
+        assert deferred.save_kv_layer(name, cache, saves) == 0
+    assert deferred.wait_for_save() == 500 * 4
+    assert deferred.wait_for_save() == 0
+    torch.cuda.synchronize(gpu)
+    assert stores[0].stats() == stores[1].stats()
+    for name in kv:
+        assert torch.equal(stores[0].read("s", name, 0, 500), stores[1].read("s", name, 0, 500))
