@@ -288,3 +288,45 @@ def test_connector_loader_fp8_with_layer_scales(gpu):
         orc.scatter_shifted(src_rows, want, ld.slots.numpy(), bs, True, -29,
                             inv_freq().numpy(), "fp8", np.float32(scales[name]))
         assert np.array_equal(bits(kv[name]), want), name
+
+
+def test_more_spans_than_one_launch_takes(gpu):
+    """5,000 short spans (some empty), past the 4,096-span launch limit: the plan splits
+    them into launches that share one workspace in stream order; every destination byte
+    against the oracle."""
+    from marathon_amd import _lib
+    from marathon_amd.spans import CacheSet, ShiftPlan
+
+    print("case 5,000 spans in two launches", flush=True)
+    rng = np.random.default_rng(17)
+    g = torch.Generator().manual_seed(17)
+    layers, heads, d, bs, n_spans = 2, 8, 128, 16, 5000
+    lens = rng.integers(0, 4, n_spans)
+    hist = [4096, 3000]
+    bufs = [[torch.randn(h, heads, 2 * d, generator=g).to(torch.bfloat16).to(gpu)
+             for _ in range(layers)] for h in hist]
+    total = int(lens.sum())
+    blocks = -(-total // bs) + 4
+    kv = [torch.randn(blocks, heads, bs, 2 * d, generator=g).to(torch.bfloat16).to(gpu)
+          for _ in range(layers)]
+    dst_slots = torch.from_numpy(rng.permutation(blocks * bs)[:total].astype(np.int64))
+    rows, off = [], 0
+    for i, n in enumerate(lens):
+        grp = int(rng.integers(2))
+        src = int(rng.integers(0, hist[grp] - 4))
+        rows.append((src, 0, 0, off, int(n), int(rng.integers(-3000, 3000)), grp, 0))
+        off += int(n)
+    assert n_spans > _lib.MKV_MAX_SPANS
+    plan = ShiftPlan(span_array(rows), CacheSet(bufs, "flat"), CacheSet([kv], "hnd", bs),
+                     inv_freq=inv_freq(), src_mode="flat", dst_mode="slots",
+                     dst_index=dst_slots)
+    assert len(plan.descs) == 2
+    src_o = oracle_side(plan.src, "flat", None)
+    dst_o = oracle_side(plan.dst, "slots", dst_slots)
+    orc.shift_spans(oracle_spans(span_array(rows)), src_o, dst_o, inv_freq().numpy(), "bf16")
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer in range(layers):
+        assert np.array_equal(bits(kv[layer]), dst_o.caches[0][layer]), f"layer {layer}"
