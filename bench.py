@@ -13,11 +13,15 @@ Prints one JSON line.  Also measured, in the same line:
   stream, against the 8 TB/s HBM peak; ``traffic`` from the committed rocprofv3
   FETCH_SIZE/WRITE_SIZE profile of this kernel and workload, when present.
 * ``cpu_baseline``: the reference's torch shift path (its op sequence, restated in
-  ``oracle/torch_path.py``) on the host CPU, on the Qwen3-0.6B-shaped config
-  (28 layers x 4,096 tokens, delta +37), best of 3 after a warmup.
+  ``oracle/torch_path.py``) on the host CPU over the headline workload itself (all 40
+  layers and 8 spans), best of 3 after a warm-up; the Qwen3-0.6B-shaped CPU case
+  (28 layers x 4,096 tokens, delta +37) is reported beside it.
 * ``reference_shape``: the reference benchmark's own shape (30,720 tokens x 40 layers,
   delta 186, flat store -> HND paged cache, scattered block table), for comparison with
-  its published 6.54 ms on an RTX 5090.
+  its published 6.54 ms on an RTX 5090, as one batched launch.
+* ``reference_loop``: the reference benchmark's own loop through the drop-in API: 40
+  per-layer ``scatter_shifted`` calls per shift at 4,096, 12,288 and 30,720 tokens, the
+  rows of its published table.
 """
 
 from __future__ import annotations
@@ -213,6 +217,71 @@ def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def reference_loop(dev, iters: int = 5) -> dict:
+    """The reference micro-benchmark's own loop through the drop-in API
+    (scripts/bench_shift_copy.py:24-53): for each of 40 layers, one ``scatter_shifted``
+    call from a ``[n, 8, 256]`` bf16 store slice into an HND paged cache through a
+    scattered slot mapping, delta 186.  Host wall clock around the 40 calls
+    (synchronised on both sides), best of ``iters`` passes after one warm-up; bytes are
+    the source read once plus the destination written once.  One row per token count
+    of its published table (docs/findings.md:644-646, RTX 5090)."""
+    import numpy as np
+    import torch
+
+    from marathon_amd.shift_kernels import inv_freq_for, rope_shift, scatter_shifted
+    from oracle import kvshift_oracle as orc
+
+    layers, heads, d, bs = 40, 8, 128, 16
+    inv = inv_freq_for(d, 1e6)
+    shift = rope_shift(186, d, inv, dev)
+    published = {4096: 1.01, 12288: 2.80, 30720: 6.54}
+    out = {"what": "40 per-layer scatter_shifted calls per shift (the reference's call "
+           "pattern), best of %d after 1 warm-up, host wall clock" % iters}
+    for n, ref_ms in published.items():
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(n)
+        blocks = -(-n // bs) + 8
+        src = [torch.randn(n, heads, 2 * d, dtype=torch.bfloat16, device=dev, generator=gen)
+               for _ in range(layers)]
+        kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
+              for _ in range(layers)]
+        table = torch.randperm(blocks, device=dev, generator=gen)
+        pos = torch.arange(n, device=dev)
+        slots = table[pos // bs] * bs + pos % bs
+        best = host = float("inf")
+        for i in range(iters + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for s, k in zip(src, kv):
+                scatter_shifted(s, k, slots, bs, True, shift)
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3
+            if i:
+                best = min(best, ms)
+                host = min(host, (t1 - t0) * 1e3)
+        # one sampled row of the last layer against the oracle
+        t = int(np.random.default_rng(n).integers(n))
+        slot = int(slots[t])
+        sb = src[-1][t].cpu().view(torch.int16).numpy().view(np.uint16)
+        gb = kv[-1][slot // bs, :, slot % bs].cpu().view(torch.int16).numpy().view(np.uint16)
+        if not (np.array_equal(gb[:, :d], orc.rotate_k_bits(sb[:, :d], 186, inv.numpy(), "bf16"))
+                and np.array_equal(gb[:, d:], sb[:, d:])):
+            raise AssertionError(f"reference loop output differs from the oracle at n={n}")
+        moved = 2 * sum(s.numel() * s.element_size() for s in src)
+        out[f"tokens_{n}"] = {
+            "ms": round(best, 4),
+            "GB_s": round(moved / (best / 1e3) / 1e9, 1),
+            "GiB_s": round(moved / (best / 1e3) / 2**30, 1),
+            "us_per_token": round(best * 1e3 / n, 4),
+            "host_enqueue_ms": round(host, 4),
+            "reference_rtx5090_ms": ref_ms,
+        }
+        del src, kv, slots, table
+        torch.cuda.empty_cache()
+    return out
+
+
 def other_workloads(dev, steps: int, warmup: int, stream) -> dict:
     """Informational: the other GPU workloads, one launch per step each."""
     import numpy as np
@@ -400,6 +469,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-shape", action="store_true")
+    ap.add_argument("--no-reference-loop", action="store_true",
+                    help="skip the reference benchmark's per-layer scatter_shifted loop")
     ap.add_argument("--no-other-workloads", "--no-other-configs", dest="no_other_workloads",
                     action="store_true",
                     help="skip the informational timings of the Qwen3-8B single-span, fp8 "
@@ -457,11 +528,14 @@ def main() -> int:
             traffic = json.load(f).get("traffic_bytes_per_launch")
 
     extra = {}
+    del wl, plan  # the headline workload's caches make room for the other sections
+    torch.cuda.empty_cache()
     if not args.no_reference_shape:
-        del wl, plan
-        torch.cuda.empty_cache()
         log("reference benchmark shape (30,720 x 40, delta 186)")
         extra["reference_shape"] = reference_shape(dev, max(5, args.steps // 2), args.warmup, stream)
+    if not args.no_reference_loop:
+        log("reference benchmark loop (40 x scatter_shifted, 4,096 / 12,288 / 30,720 tokens)")
+        extra["reference_loop"] = reference_loop(dev)
     if not args.no_other_workloads:
         extra["other_workloads"] = other_workloads(dev, max(5, args.steps // 2), args.warmup,
                                                    stream)

@@ -123,7 +123,16 @@ def paged_strides(kv: torch.Tensor, hnd: bool) -> tuple[int, int, int]:
     return (s[0], s[1], s[2]) if hnd else (s[0], s[2], s[1])
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def current_stream(device: torch.device) -> int:
+    """The hipStream_t of ``device``'s current stream, as an integer.  Read through
+    torch's raw-stream accessor where this torch has it (0.06 us instead of the 1.9 us
+    of building a ``torch.cuda.Stream`` object: a per-layer call pays this 40 times)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return int(_raw_stream(idx))
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
@@ -192,29 +201,34 @@ def scatter_shifted(
                 raise ValueError("fp8 KV cache needs k_scale")
             scale = _scale_tensor(k_scale, kv.device)
     blk_s, head_s, off_s = paged_strides(kv, hnd)
-    with torch.cuda.device(kv.device):
-        rc = _lib.lib().mkv_scatter_shifted(
-            src.data_ptr(),
-            src.stride(0),
-            src.stride(1),
-            kv.data_ptr(),
-            blk_s,
-            head_s,
-            off_s,
-            kv.shape[0],
-            slots.data_ptr(),
-            n,
-            heads,
-            d,
-            int(block_size),
-            code,
-            _ptr(cos),
-            _ptr(sgn),
-            shift.rotary if rotate else 0,
-            _ptr(scale),
-            _ptr(error_flags),
-            ctypes.c_void_p(current_stream(kv.device)),
-        )
+    args = (
+        src.data_ptr(),
+        src.stride(0),
+        src.stride(1),
+        kv.data_ptr(),
+        blk_s,
+        head_s,
+        off_s,
+        kv.shape[0],
+        slots.data_ptr(),
+        n,
+        heads,
+        d,
+        int(block_size),
+        code,
+        _ptr(cos),
+        _ptr(sgn),
+        shift.rotary if rotate else 0,
+        _ptr(scale),
+        _ptr(error_flags),
+        ctypes.c_void_p(current_stream(kv.device)),
+    )
+    fn = _lib.lib().mkv_scatter_shifted
+    if kv.device.index == torch.cuda.current_device():
+        rc = fn(*args)
+    else:
+        with torch.cuda.device(kv.device):  # the launch goes to the current device
+            rc = fn(*args)
     _lib.check(rc)
 
 

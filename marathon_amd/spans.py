@@ -311,19 +311,26 @@ class ShiftPlan:
         with a device synchronisation)."""
         if stream is None:
             stream = current_stream(self.device)
+        if self.device.index == torch.cuda.current_device():
+            self._launch(int(stream), error_flags)
+        else:
+            with torch.cuda.device(self.device):  # launches go to the current device
+                self._launch(int(stream), error_flags)
+
+    def _launch(self, stream: int, error_flags: torch.Tensor | None) -> None:
         L = _lib.lib()
-        with torch.cuda.device(self.device):
-            if int(stream) not in self._synced:
-                # the tables were copied on the stream current at build time
-                ext = torch.cuda.ExternalStream(int(stream), device=self.device)
-                if not torch.cuda.is_current_stream_capturing():
-                    ext.wait_event(self._ready)
-                for t in (*self._keep, self.workspace):
-                    t.record_stream(ext)
-                self._synced.add(int(stream))
-            for d in self.descs:
-                d.error_flags = error_flags.data_ptr() if error_flags is not None else None
-                _lib.check(L.mkv_shift_spans(ctypes.byref(d), ctypes.c_void_p(stream)))
+        if stream not in self._synced:
+            # the tables were copied on the stream current at build time
+            ext = torch.cuda.ExternalStream(stream, device=self.device)
+            if not torch.cuda.is_current_stream_capturing():
+                ext.wait_event(self._ready)
+            for t in (*self._keep, self.workspace):
+                t.record_stream(ext)
+            self._synced.add(stream)
+        flags = error_flags.data_ptr() if error_flags is not None else None
+        for d in self.descs:
+            d.error_flags = flags
+            _lib.check(L.mkv_shift_spans(ctypes.byref(d), ctypes.c_void_p(stream)))
 
 
 def span_array(rows) -> np.ndarray:
