@@ -176,6 +176,8 @@ typedef struct mkv_shift_desc {
  * rotary    : rotated dimensions (2 * len(inv_freq)); dims >= rotary are copied.
  *             n_tokens == 0 is a no-op.
  * k_scale   : device fp32 [1] for MKV_FP8_E4M3 when rotating, else NULL.
+ * Tokens move concurrently, as in the Triton kernel: a slot repeated in `slots` gets
+ * one of its tokens, which one is unspecified; `src` must not alias `kv`.
  */
 int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_head_stride,
                         void* kv, int64_t kv_block_stride, int64_t kv_head_stride,
@@ -190,6 +192,11 @@ int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_h
  * connector's per-load, per-layer loop of store.read + scatter_shifted
  * (src/marathon/vllm_shift_connector.py:481-534, loop at :505-518) and the HF
  * prototype's per-segment stitch (src/marathon/kvshift.py:242-268, :265-266).
+ * Every row of every span and layer moves concurrently: destination rows must be
+ * distinct, and no destination row may also be read as a source row by the same call.
+ * If two rows share a destination, which one lands is unspecified.  The reference's
+ * sequential loop lets the later load win, but its loads cover disjoint destination
+ * ranges.
  */
 int mkv_shift_spans(const mkv_shift_desc_t* desc, void* stream);
 
