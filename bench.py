@@ -465,7 +465,7 @@ def save_step(dev, steps: int, warmup: int) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-shape", action="store_true")
@@ -528,22 +528,23 @@ def main() -> int:
             traffic = json.load(f).get("traffic_bytes_per_launch")
 
     extra = {}
+    side_steps = max(5, min(args.steps, 20))  # the informational sections
     del wl, plan  # the headline workload's caches make room for the other sections
     torch.cuda.empty_cache()
     if not args.no_reference_shape:
         log("reference benchmark shape (30,720 x 40, delta 186)")
-        extra["reference_shape"] = reference_shape(dev, max(5, args.steps // 2), args.warmup, stream)
+        extra["reference_shape"] = reference_shape(dev, side_steps, args.warmup, stream)
     if not args.no_reference_loop:
         log("reference benchmark loop (40 x scatter_shifted, 4,096 / 12,288 / 30,720 tokens)")
         extra["reference_loop"] = reference_loop(dev)
     if not args.no_other_workloads:
-        extra["other_workloads"] = other_workloads(dev, max(5, args.steps // 2), args.warmup,
+        extra["other_workloads"] = other_workloads(dev, side_steps, args.warmup,
                                                    stream)
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
-        extra["connector_step"] = connector_step(dev, max(5, args.steps), args.warmup)
+        extra["connector_step"] = connector_step(dev, side_steps, args.warmup)
         log("connector save step (paged -> block store)")
-        extra["save_step"] = save_step(dev, max(5, args.steps), args.warmup)
+        extra["save_step"] = save_step(dev, side_steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (reference torch path on the host, the Qwen3-14B multi-span shift)")
