@@ -125,6 +125,36 @@ def test_block_sizes(gpu, bs):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("dtype,heads,d,rotary,hnd", [
+    (torch.bfloat16, 2, 512, 512, True),       # a K row fills a whole wave (64 chunks)
+    (torch.float32, 4, 256, 256, False),       # fp32: a K row fills a whole wave
+    (torch.bfloat16, 64, 128, 128, True),      # one token is 8 passes of a workgroup
+    (torch.float16, 32, 64, 64, False),        # 8 rows per wave, 2 passes per token
+    (torch.float8_e4m3fn, 8, 64, 64, False),   # fp8: 16 rows per wave span two tokens
+    (torch.float8_e4m3fn, 3, 256, 128, True),  # fp8: ragged heads, partial rotary
+])
+def test_geometry_limits(gpu, dtype, heads, d, rotary, hnd):
+    """The largest head size (512), rows that fill a whole wave, many heads (one token
+    over several passes) and waves whose rows span tokens, in every element type."""
+    print(f"case geometry {dtype} heads={heads} d={d} rotary={rotary} hnd={hnd}", flush=True)
+    g = torch.Generator().manual_seed(heads * 1000 + d + rotary)
+    scale, n, nblocks, delta = 0.05, 37, 16, -301
+    src = randn((n, heads, 2 * d), dtype, g, scale)
+    shape = (nblocks, heads, 16, 2 * d) if hnd else (nblocks, 16, heads, 2 * d)
+    kv = randn(shape, dtype, g, scale)
+    table = torch.randperm(nblocks, generator=g)
+    pos = torch.arange(7, 7 + n)
+    slots = table[pos // 16] * 16 + pos % 16
+    inv = inv_freq(rotary)
+    fp8 = dtype == torch.float8_e4m3fn
+    got = bits(_run_gpu(gpu, src, kv, slots, 16, hnd, rope_shift(delta, d, inv, gpu),
+                        **({"k_scale": scale} if fp8 else {})))
+    want = bits(kv)
+    orc.scatter_shifted(bits(src), want, slots.numpy(), 16, hnd, delta, inv.numpy(),
+                        dname(dtype), **({"k_scale": np.float32(scale)} if fp8 else {}))
+    assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
+
+
 def test_source_view_into_a_store_buffer(gpu):
     """The connector hands the kernel ``buf[start:start+n]`` of a store buffer."""
     g = torch.Generator().manual_seed(3)

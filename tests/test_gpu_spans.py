@@ -148,6 +148,11 @@ def _two_session_plan(gpu, dtype, heads, d, rotary, seed, spans, table, k_scale=
     (torch.bfloat16, 3, 64, 64),
     (torch.bfloat16, 5, 256, 128),
     (torch.float8_e4m3fn, 5, 128, 128),
+    (torch.bfloat16, 2, 512, 512),       # a K row fills a whole wave
+    (torch.float32, 4, 256, 256),        # fp32: a K row fills a whole wave
+    (torch.bfloat16, 64, 128, 128),      # one token is 8 passes of a workgroup
+    (torch.float8_e4m3fn, 8, 64, 64),    # fp8: 16 rows per wave span two tokens
+    (torch.float8_e4m3fn, 3, 256, 128),  # fp8: ragged heads, partial rotary
 ])
 def test_batched_other_geometries_match_oracle(gpu, dtype, heads, d, rotary):
     """Non-uniform head counts (a wave pass spans tokens), partial rotary, fp16 / fp32 /
