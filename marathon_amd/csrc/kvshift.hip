@@ -70,6 +70,12 @@
 #ifndef MKV_TABLE_WITH_DATA
 #define MKV_TABLE_WITH_DATA 1
 #endif
+// Cache policy of the shift kernel's stores where the destination row is wave-uniform
+// (buffer stores): 18 = sc1 | nt (device-scope streaming).  -1: plain non-temporal
+// global stores everywhere.
+#ifndef MKV_STORE_CPOL
+#define MKV_STORE_CPOL 18
+#endif
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs; with
 // the remap, XCD k walks the k-th contiguous eighth of the tiles (smaller per-XCD set
 // of pages in flight).  0 = plain order.
@@ -82,6 +88,11 @@ namespace {
 constexpr int kThreads = MKV_WG_THREADS;  // shift kernel; a multiple of the 64-lane wave
 constexpr int kWaves = kThreads / 64;
 constexpr int kPlanThreads = 256;  // plan kernel
+// Buffer resources for the stores: raw (stride 0), the whole 32-bit range checked by
+// the hardware (a lane's offset is below 2^31, checked on the host), and the gfx9
+// default data-format word.
+constexpr int kRsrcRange = -1;  // 0xFFFFFFFF bytes
+constexpr int kRsrcWord3 = 0x00020000;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Global-address-space view: keeps the compiler on global_load/global_store rather
@@ -217,6 +228,21 @@ __device__ __forceinline__ void store16(char* p, u32x4 v) {
   __builtin_nontemporal_store(v, (g_u32x4*)p);
 #else
   *(g_u32x4*)p = v;
+#endif
+}
+
+// Store through a buffer resource whose base is wave-uniform (`base`, a row of the
+// destination) at a per-lane 32-bit offset, with the cache policy MKV_STORE_CPOL.  The
+// default, device-scope streaming (sc1 nt), measured 2-3% faster than nt alone on gfx950
+// for these write-once rows; the global-store builtins cannot set the scope bits.
+// Policy bits: 1 sc0, 2 nt, 16 sc1.
+__device__ __forceinline__ void store16_at(char* base, uint32_t lane_off, u32x4 v) {
+#if MKV_STORE_CPOL >= 0
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(base, 0, kRsrcRange, kRsrcWord3);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(lane_off), 0, MKV_STORE_CPOL);
+#else
+  store16(base + lane_off, v);
 #endif
 }
 
@@ -728,14 +754,22 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       }
     }
 
-    // ---- phase D: stores
+    // ---- phase D: stores (UNIFORM: the pass's destination row is wave-uniform, so the
+    // stores go through buffer resources carrying the store cache policy)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (live[u] && lane_live) {
-        store16(dbk[u] + d_at[u] + d_lane, kd[u]);
+        if constexpr (UNIFORM) {
+          store16_at(dbk[u] + d_at[u], d_lane, kd[u]);
 #if !MKV_V_FIRST
-        store16(dbv[u] + d_at[u] + d_lane, vd[u]);
+          store16_at(dbv[u] + d_at[u], d_lane, vd[u]);
 #endif
+        } else {
+          store16(dbk[u] + d_at[u] + d_lane, kd[u]);
+#if !MKV_V_FIRST
+          store16(dbv[u] + d_at[u] + d_lane, vd[u]);
+#endif
+        }
       }
     }
   }
