@@ -482,7 +482,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(
-            "bench.py measures one GPU: the shift needs no collective and this build runs on "
+            "bench.py measures one GPU: the shift needs no collective and this library runs on "
             "a single MI355X (per-rank sharding is by KV head / layer / session with no "
             "exchange).  Run with --gpus 1.",
             file=sys.stderr,

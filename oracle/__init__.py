@@ -13,7 +13,7 @@ HIP kernels can be checked against it:
   the kernels against (within 1 bf16 ulp).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker or the baseline -- never
+``bench.py`` may import this package, and only to check results or as the baseline -- never
 as the thing measured or shipped.  The product (``marathon_amd``) never imports it and
 has no CPU fallback.
 

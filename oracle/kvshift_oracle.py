@@ -45,7 +45,8 @@ def f32_to_bf16(x: np.ndarray) -> np.ndarray:
     The rounding of every non-NaN value is torch's ``.to(torch.bfloat16)``, which is
     what ``scatter_shifted_torch`` applies to the rotated K (shift_kernels.py:156).  NaN
     payloads are implementation-defined there (c10's scalar cast gives 0x7FC0, the
-    vectorized CPU cast keeps payload bits); this build canonicalises to 0x7FC0.
+    vectorized CPU cast keeps payload bits); the kernels and this oracle canonicalise to
+    0x7FC0.
     """
     x = np.asarray(x, np.float32)
     u = x.view(np.uint32).astype(np.uint64)
@@ -232,7 +233,7 @@ def rotate_k_bits(
     flag, :124, :187).  Dimensions at or above ``rotary`` pass through untouched
     (shift_kernels.py:74-75 gives them cos 1, sgn 0).  bf16/fp16/fp32: upcast, rotate in
     fp32, round to nearest even (shift_kernels.py:153-156).  fp8 e4m3fn (no reference
-    -- this build's rule): x = fl32(decode * s); rotate; q = fl32(y / s) clamped to
+    -- the kernels' own rule): x = fl32(decode * s); rotate; q = fl32(y / s) clamped to
     +-448 (NaN kept), encoded round-to-nearest-even.
     """
     k_bits = np.asarray(k_bits)

@@ -82,7 +82,7 @@ def test_bf16_rounding_matches_torch():
     nan = np.isnan(x)
     assert np.array_equal(got[~nan], want[~nan])
     # NaN payloads are implementation-defined (torch's vectorized CPU cast keeps payload
-    # bits, c10's scalar cast returns 0x7FC0); this build canonicalises every NaN
+    # bits, c10's scalar cast returns 0x7FC0); the kernels canonicalise every NaN
     assert np.all(got[nan] == 0x7FC0)
     assert np.all((want[nan] & 0x7F80) == 0x7F80) and np.all(want[nan] & 0x007F)
     # and upcasting is exact
