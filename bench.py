@@ -563,6 +563,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
+        "arithmetic": "K rotated in fp32 (mul, mul, add, no FMA) and rounded to bf16 (RNE); "
+        "V copied as raw bytes",
         "data": "synthetic: K/V ~ N(0,1) bf16 drawn on device (seed 3), shuffled block tables",
         "config": {
             "workload": "qwen3-14b multi-span shift: 40 layers, 8 kv heads, head_dim 128, "
