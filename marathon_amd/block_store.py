@@ -107,6 +107,7 @@ class BlockShiftStore:
         self._sessions: OrderedDict[str, _BlockEntry] = OrderedDict()  # oldest first
         self._free = list(range(self.pool_blocks))  # a heap: lowest id first
         self._pools: dict[str, torch.Tensor] = {}
+        self._sigs: dict[str, tuple] = {}  # layer -> (row shape, dtype) of its pool
         self.hits = 0
         self.misses = 0
         self.evictions = 0
@@ -133,12 +134,15 @@ class BlockShiftStore:
         return len(self._free)
 
     def _release(self, entry: _BlockEntry, lo_block: int, hi_block: int) -> None:
-        part = entry.table[max(lo_block, 0):max(min(hi_block, entry.table.size), 0)]
-        freed = part[part >= 0]
-        for b in freed.tolist():
-            heapq.heappush(self._free, b)
-        entry.held -= int(freed.size)
-        part[:] = -1
+        if max(lo_block, 0) < min(hi_block, entry.table.size):
+            part = entry.table[max(lo_block, 0):min(hi_block, entry.table.size)]
+            freed = part[part >= 0]
+            for b in freed.tolist():
+                heapq.heappush(self._free, b)
+            entry.held -= int(freed.size)
+            part[:] = -1
+        elif entry.table.size == 0 or entry.table[-1] >= 0:
+            return  # nothing in the range and no unheld tail to trim (an append)
         live = np.flatnonzero(entry.table >= 0)
         entry.table = entry.table[: int(live[-1]) + 1 if live.size else 0]
 
@@ -150,7 +154,10 @@ class BlockShiftStore:
         if entry.table.size < k1:
             entry.table = np.concatenate(
                 (entry.table, np.full(k1 - entry.table.size, -1, dtype=np.int32)))
-        missing = k0 + np.flatnonzero(entry.table[k0:k1] < 0)
+        if k1 - k0 <= 2:  # a decode step's save: one or two blocks, no numpy needed
+            missing = np.array([k for k in range(k0, k1) if entry.table[k] < 0], dtype=np.int64)
+        else:
+            missing = k0 + np.flatnonzero(entry.table[k0:k1] < 0)
         while len(self._free) < missing.size:
             victim = next((s for s in self._sessions if s != session), None)
             if victim is None:
@@ -210,13 +217,15 @@ class BlockShiftStore:
         return self._pools.get(layer)
 
     def _pool_for(self, layer: str, row_shape, dtype, device) -> torch.Tensor:
+        sig = (tuple(row_shape), dtype)
         p = self._pools.get(layer)
         if p is None:
-            p = torch.zeros((self.pool_blocks, self.block_size, *row_shape), dtype=dtype,
+            p = torch.zeros((self.pool_blocks, self.block_size, *sig[0]), dtype=dtype,
                             device=device)
             self._pools[layer] = p
-        elif tuple(p.shape[2:]) != tuple(row_shape) or p.dtype != dtype:
-            raise ValueError(f"layer {layer}: rows {tuple(row_shape)} {dtype} do not match "
+            self._sigs[layer] = sig
+        elif self._sigs[layer] != sig:
+            raise ValueError(f"layer {layer}: rows {sig[0]} {dtype} do not match "
                              f"the pool's {tuple(p.shape[2:])} {p.dtype}")
         return p
 
@@ -248,11 +257,12 @@ class BlockShiftStore:
         entry = self._sessions.get(session)
         if not self._positions_ok(entry, dst_start, n):
             return None
-        out = []
-        for layer in layers:
-            out.append(self._pool_for(layer, row_shape, dtype, device))
-            entry.layers.add(layer)
-            self.saved_token_layers += n
+        sig = (tuple(row_shape), dtype)
+        pools, sigs = self._pools, self._sigs
+        out = [pools[layer] if sigs.get(layer) == sig else
+               self._pool_for(layer, row_shape, dtype, device) for layer in layers]
+        entry.layers.update(layers)
+        self.saved_token_layers += n * len(out)
         return out
 
     def write_target(

@@ -97,15 +97,16 @@ class CacheSet:
         return t.shape[0] * (1 if self.layout == "flat" else self.block_size)
 
     def base_tables(self):
-        """``(k, v, caps)``: per-(group, layer) K and V base addresses (uint64) and
-        per-group slot capacities, computed once per CacheSet."""
+        """``(k, v, caps, min_cap, uniform)``: per-(group, layer) K and V base addresses
+        (uint64), per-group slot capacities, their minimum and whether they are all
+        equal; computed once per CacheSet."""
         got = getattr(self, "_bases", None)
         if got is None:
             eb = self.first.element_size()
             k = np.array([[t.data_ptr() for t in row] for row in self.caches], dtype=np.uint64)
             v = k + np.uint64(self.head_size * eb)
             caps = np.array([self.slots_of(row[0]) for row in self.caches], dtype=np.int64)
-            got = self._bases = (k, v, caps)
+            got = self._bases = (k, v, caps, int(caps.min()), bool(np.all(caps == caps[0])))
         return got
 
 
@@ -173,7 +174,10 @@ class ShiftPlan:
             raise ValueError("src and dst on different devices")
         self.src, self.dst = src, dst
         self.n_spans = int(spans.shape[0])
-        self.tokens = int(np.maximum(spans["n_tokens"], 0).sum()) if self.n_spans else 0
+        # per-span token counts as Python ints (numpy reductions cost more on the few
+        # spans of a step than the sums themselves)
+        counts = [max(int(c), 0) for c in spans["n_tokens"].tolist()]
+        self.tokens = sum(counts)
         self.dtype = dtype_code(dst.first.dtype)
         self._keep: list = []
         stage = _Staging()
@@ -204,14 +208,19 @@ class ShiftPlan:
         src_plan = self._side(src, src_mode, src_index, stage, place)
         dst_plan = self._side(dst, dst_mode, dst_index, stage, place)
         span_off = stage.add(spans.view(np.uint8).reshape(-1)) if self.n_spans else None
-        with torch.cuda.device(self.device):
+        # the tables are copied on the device's current stream; a launch on another
+        # stream first waits for this event (see _launch)
+        if self.device.index == torch.cuda.current_device():
             blob = stage.upload(self.device)
-            # launches on another stream first wait for this copy (see launch)
-            self._build_stream = torch.cuda.current_stream(self.device)
             self._ready = torch.cuda.Event()
-            self._ready.record(self._build_stream)
+            self._ready.record()
+        else:
+            with torch.cuda.device(self.device):
+                blob = stage.upload(self.device)
+                self._ready = torch.cuda.Event()
+                self._ready.record()
         self._keep.append(blob)
-        self._synced = {int(self._build_stream.cuda_stream)}
+        self._synced = {current_stream(self.device)}
         base = blob.data_ptr()
 
         def ptr(item) -> int | None:
@@ -225,11 +234,10 @@ class ShiftPlan:
 
         self.descs = []
         step = _lib.MKV_MAX_SPANS
-        counts = np.maximum(spans["n_tokens"].astype(np.int64), 0) if self.n_spans else None
         chunks = [(lo, min(step, self.n_spans - lo)) for lo in range(0, self.n_spans, step)]
         L = _lib.lib()
         need = max(
-            (L.mkv_shift_workspace_size(int(counts[lo:lo + cnt].sum()), cnt, self.rotary)
+            (L.mkv_shift_workspace_size(sum(counts[lo:lo + cnt]), cnt, self.rotary)
              for lo, cnt in chunks),
             default=0,
         )
@@ -240,7 +248,7 @@ class ShiftPlan:
             d.spans = base + span_off + lo * _lib.SPAN_DTYPE.itemsize
             d.workspace = self.workspace.data_ptr()
             d.workspace_bytes = self.workspace.numel()
-            d.total_tokens = int(counts[lo:lo + cnt].sum())
+            d.total_tokens = sum(counts[lo:lo + cnt])
             d.inv_freq = ptr(inv)
             d.k_scale = ptr(scale)
             d.error_flags = None
@@ -258,14 +266,14 @@ class ShiftPlan:
     def _side(cs: CacheSet, mode: str, index, stage: _Staging, place) -> dict:
         if mode not in MODES:
             raise ValueError(f"mode {mode!r}")
-        k, v, caps = cs.base_tables()
+        k, v, caps, min_cap, uniform = cs.base_tables()
         out = {
             "cs": cs,
             "mode": mode,
             "k": (None, stage.add(k.reshape(-1)), k.size),
             "v": (None, stage.add(v.reshape(-1)), v.size),
-            "num_slots": int(caps.min()),
-            "group_slots": None if np.all(caps == caps[0]) else (None, stage.add(caps), caps.size),
+            "num_slots": min_cap,
+            "group_slots": None if uniform else (None, stage.add(caps), caps.size),
             "index": (None, None, 0),
         }
         if mode != "flat":
