@@ -234,6 +234,32 @@ def test_single_span_out_of_range_slot_is_flagged_and_skipped(gpu):
     assert torch.equal(kv.view(torch.int16), kv_ok.view(torch.int16))
 
 
+def test_plan_launched_on_another_stream(gpu):
+    """A plan built on the current stream (its tables copied there) and launched at once
+    on a side stream, with no host synchronisation in between: the launch waits for the
+    copy's event and keeps the plan's buffers alive on that stream.  Every destination
+    byte against the oracle, then a second launch on the same side stream."""
+    print("case plan launched on a side stream", flush=True)
+    wl = W.qwen3_14b_multispan(gpu, layers=2, history=1024, dst_fill="random")
+    src_o = oracle_side(wl.src, wl.src_mode, wl.src_index)
+    dst_o = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
+    orc.shift_spans(oracle_spans(wl.spans), src_o, dst_o, wl.inv_freq.numpy(), "bf16")
+    torch.cuda.synchronize(gpu)
+    side = torch.cuda.Stream(device=gpu)
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    torch.cuda.synchronize(gpu)
+    # the caches and flags are complete (synchronised above); the plan's tables are
+    # copied on the current stream, and only the plan's own event orders that copy
+    # before the side-stream launch
+    plan = wl.plan()
+    plan.launch(side.cuda_stream, error_flags=flags)
+    plan.launch(side.cuda_stream, error_flags=flags)  # a second launch: same bytes
+    side.synchronize()
+    assert int(flags.item()) == 0
+    for layer, t in enumerate(wl.dst.caches[0]):
+        assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
+
+
 def test_plan_launch_replays_from_a_hip_graph(gpu):
     """A captured launch replays exactly like an eager one: three replays, with eager
     work between them (new source values, a cleared destination, an eager launch that
