@@ -26,7 +26,14 @@
 //     and destination row (slot arrays / block tables, bounds-checked) into a record,
 //     and evaluates each span's cos/sin once (double precision, rounded to fp32).
 //     Both live in a caller-provided workspace; the library allocates nothing.
-//   * Loads and stores are non-temporal: every byte is touched exactly once.
+//   * Loads and stores are non-temporal: every byte is touched exactly once.  Where a
+//     pass's destination row is wave-uniform, the stores also carry device scope
+//     (sc1 nt, through a buffer resource), measured 2-3% faster for these write-once
+//     rows.
+//   * Workgroups move one token each (bf16: 128 threads = 8 rows of 512 B) and are
+//     dealt so that each XCD walks one contiguous range of tokens, layer by layer:
+//     measured against every other order tried (strided ranges, layers inner,
+//     persistent walks), this is the fastest.
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
