@@ -25,6 +25,7 @@ block tables.
 from __future__ import annotations
 
 import logging
+import os
 import time
 from dataclasses import dataclass
 
@@ -37,6 +38,47 @@ from .shift_store import ShiftStore, slots as host_slots
 from .spans import CacheSet, ShiftPlan
 
 logger = logging.getLogger("marathon_amd.shift")
+
+#: ``MARATHON_VERIFY_LOAD=1`` reads every loaded span back out of the paged cache and
+#: compares it with torch's rotation of the same source rows, per layer, and logs the
+#: error (vllm_shift_connector.py:95-102, :444-480).  Diagnostic only, off by default:
+#: it reads, it never writes a cache, and the kernel still does every load.
+VERIFY_LOAD = os.environ.get("MARATHON_VERIFY_LOAD", "") not in ("", "0")
+
+
+def store_from_config(extra: dict | None, worker: bool, *, block_layout: bool = False,
+                      block_size: int = 16):
+    """The connector's store, configured as the reference's connector configures it
+    (vllm_shift_connector.py:168-178): budget from ``kv_connector_extra_config``
+    ``store_tokens``, else ``MARATHON_STORE_TOKENS``, else 32,768; ``store_device``;
+    ``session_tokens`` (one session's positions, allocated once).  Tensors only on the
+    worker; the scheduler keeps the tensor-free mirror.  ``block_layout`` returns the
+    :class:`BlockShiftStore` with the reference's truncation rule instead."""
+    from .shift_store import DEFAULT_STORE_TOKENS
+
+    extra = extra or {}
+    budget = int(extra.get("store_tokens", os.environ.get("MARATHON_STORE_TOKENS",
+                                                          DEFAULT_STORE_TOKENS)))
+    device = str(extra.get("store_device", "cuda"))
+    if block_layout:
+        return BlockShiftStore(budget, device, allocate=worker, block_size=block_size)
+    cap = int(extra.get("session_tokens", 0) or 0)
+    return ShiftStore(budget, device, allocate=worker, session_cap=cap)
+
+
+def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def _rerotate(k: torch.Tensor, delta: int, inv_freq: torch.Tensor) -> torch.Tensor:
+    """torch's rotation of fp32 keys by ``delta``: the reference's ``rerotate_keys``
+    (kvshift.py:44-61), here only the yardstick of the read-back check."""
+    if delta == 0:
+        return k
+    angles = float(delta) * inv_freq.to(device=k.device, dtype=torch.float32)
+    emb = torch.cat((angles, angles), dim=-1)
+    return k * emb.cos() + _rotate_half(k) * emb.sin()
 
 
 @dataclass
@@ -201,8 +243,11 @@ class ShiftLoader:
         *,
         k_scales: dict | None = None,
         timing: bool = False,
+        verify: bool | None = None,
     ):
         self.store = store
+        self.verify = VERIFY_LOAD if verify is None else bool(verify)
+        self.verify_log: list = []  # one dict per (load, layer) checked
         self.block_size = int(block_size)
         self.inv_freq = inv_freq.detach().to(torch.float32).cpu()
         self.k_scales = k_scales or {}
@@ -297,6 +342,10 @@ class ShiftLoader:
             t0 = time.perf_counter()
         plan.launch()
         self.last_plan = plan
+        if self.verify:
+            for load in taken:
+                for name in names:
+                    self._verify(name, load, k_scale, names.index(name))
         tokens = sum(load.n for load in taken)
         if self.timing:
             torch.cuda.synchronize(dst.first.device)
@@ -310,6 +359,55 @@ class ShiftLoader:
                 plan.algorithmic_bytes / 1e9 / max(ms / 1e3, 1e-12),
             )
         return tokens * len(names)
+
+
+    def _source_rows(self, load: Load, name: str) -> torch.Tensor:
+        """``[n, heads, 2D]`` rows the load read, without the store's read accounting."""
+        n = load.n
+        if isinstance(self.store, BlockShiftStore):
+            pool = self.store.pool(name)
+            pos = torch.arange(load.src_start, load.src_start + n)
+            tab = torch.from_numpy(self.store.table(load.session).astype(np.int64))
+            bs = self.store.block_size
+            return pool[tab[pos // bs].to(pool.device), (pos % bs).to(pool.device)]
+        return self.store.buffer(load.session, name)[load.src_start:load.src_start + n]
+
+    def _verify(self, name: str, load: Load, k_scale, layer: int) -> None:
+        """Read a loaded span back and compare it with torch's rotation of its source
+        rows (vllm_shift_connector.py:444-480): K re-rotated by delta in fp32, the
+        dimensions past ``rotary`` and V as stored.  fp8 rows are compared dequantised
+        with the layer's K scale (V raw).  The figures are logged and kept in
+        :attr:`verify_log`."""
+        kv = self._kv[name]
+        row = self._source_rows(load, name)
+        d = row.shape[-1] // 2
+        rot = 2 * int(self.inv_freq.numel())
+        slots = (load.slots if load.slots is not None else
+                 host_slots(load.block_ids, load.paged_pos, load.paged_pos + load.n,
+                            self.block_size)).to(kv.device, torch.int64)
+        blk, off = slots // self.block_size, slots % self.block_size
+        got = kv[blk, :, off] if self.hnd else kv[blk, off]
+        scale = 1.0 if k_scale is None else float(k_scale[layer])
+        k = row[..., :d].to(torch.float32) * scale
+        want_k = torch.cat((_rerotate(k[..., :rot], int(load.delta), self.inv_freq),
+                            k[..., rot:]), dim=-1)
+        want = torch.cat((want_k, row[..., d:].to(torch.float32)), dim=-1)
+        got = torch.cat((got[..., :d].to(torch.float32) * scale,
+                         got[..., d:].to(torch.float32)), dim=-1)
+        diff = (got - want).abs()
+        entry = {
+            "layer": name,
+            "delta": int(load.delta),
+            "n": int(load.n),
+            "max_abs": float(diff.max()),
+            "max_rel": float(diff.max() / want.abs().max().clamp_min(1e-6)),
+            "mean_abs": float(diff.mean()),
+            "v_exact": bool(torch.equal(got[..., d:], want[..., d:])),
+        }
+        self.verify_log.append(entry)
+        logger.info("shift-verify: layer=%s delta=%d n=%d max_abs=%.4g max_rel=%.4g "
+                    "mean_abs=%.4g", name, entry["delta"], entry["n"], entry["max_abs"],
+                    entry["max_rel"], entry["mean_abs"])
 
 
 class ShiftSaver:

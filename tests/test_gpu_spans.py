@@ -321,6 +321,62 @@ def test_connector_loader_fp8_with_layer_scales(gpu):
         assert np.array_equal(bits(kv[name]), want), name
 
 
+def test_load_read_back_check(gpu):
+    """The reference's MARATHON_VERIFY_LOAD read-back (vllm_shift_connector.py:444-480),
+    on a block-store bf16 load with partial rotary and on a flat-store fp8 load with
+    per-layer K scales: one entry per (load, layer), V exact, K within half an element
+    step of torch's fp32 rotation (bf16: 2^-9 of the largest value, checked at 2^-8;
+    e4m3: 2^-4, checked at 0.07)."""
+    from marathon_amd import BlockShiftStore
+    from marathon_amd.connector import Load as L
+
+    print("case load read-back check", flush=True)
+    layers, heads, d, bs = 2, 8, 128, 16
+    names = [f"layers.{i}" for i in range(layers)]
+    g = torch.Generator().manual_seed(71)
+    # bf16, block store, rotary 64 of 128
+    store = BlockShiftStore(budget_tokens=2048, device=str(gpu), block_size=bs)
+    assert store.reserve("s", 0, 500)
+    for name in names:
+        store.write_target("s", name, 0, 500, (heads, 2 * d), torch.bfloat16,
+                           gpu).copy_(torch.randn(store.pool_blocks, bs, heads, 2 * d,
+                                                  generator=g).to(torch.bfloat16))
+    kv = {name: torch.zeros(48, heads, bs, 2 * d, dtype=torch.bfloat16, device=gpu)
+          for name in names}
+    loader = ShiftLoader(store, bs, inv_freq(64), verify=True)
+    loader.register_kv_caches(kv)
+    table = torch.randperm(48, generator=g).numpy().astype(np.int32)
+    loads = [L.from_blocks("s", table, 40, 300, -17), L.from_blocks("s", table, 310, 470, 0)]
+    loader.start_load_kv(loads)
+    torch.cuda.synchronize(gpu)
+    log = loader.verify_log
+    assert len(log) == len(loads) * layers
+    for e in log:
+        assert e["v_exact"], e
+        assert e["max_rel"] <= 2.0**-8, e
+    assert any(e["max_abs"] > 0 for e in log if e["delta"] != 0)  # a rotation happened
+    assert all(e["max_abs"] == 0 for e in log if e["delta"] == 0)  # delta 0: a copy
+
+    # fp8, flat store, per-layer scales
+    scales = {name: s for name, s in zip(names, (0.02, 0.07))}
+    fstore = ShiftStore(budget_tokens=2048, device=str(gpu), slab=512)
+    assert fstore.reserve("f", 0, 300)
+    for name in names:
+        x = (torch.randn(300, heads, 2 * d, generator=g) / scales[name]).clamp(-448, 448)
+        fstore.write("f", name, 0, x.to(torch.float8_e4m3fn).to(gpu))
+    fkv = {name: torch.zeros(32, heads, bs, 2 * d, dtype=torch.float8_e4m3fn, device=gpu)
+           for name in names}
+    floader = ShiftLoader(fstore, bs, inv_freq(), k_scales=scales, verify=True)
+    floader.register_kv_caches(fkv)
+    perm = torch.randperm(32, generator=g).tolist()
+    floader.start_load_kv([L("f", slots(perm, 5, 5 + 250, bs), src_start=30, delta=211)])
+    torch.cuda.synchronize(gpu)
+    assert len(floader.verify_log) == layers
+    for e in floader.verify_log:
+        assert e["v_exact"], e
+        assert 0 < e["max_rel"] <= 0.07, e
+
+
 def test_more_spans_than_one_launch_takes(gpu):
     """5,000 short spans (some empty), past the 4,096-span launch limit: the plan splits
     them into launches that share one workspace in stream order; every destination byte

@@ -270,3 +270,21 @@ def test_paged_index_tables_and_slots():
     assert index.tolist() == slots([7, 3, 9], 5, 40, 16).tolist() + [64, 65, 66]
     with pytest.raises(ValueError):
         paged_index([Save.from_blocks("s", [1, 2], 20, 40)], 16)  # 40 > 2 blocks
+
+
+def test_store_from_config_follows_the_reference_order(monkeypatch):
+    """Budget from extra config, else MARATHON_STORE_TOKENS, else 32,768; tensors only
+    on the worker; session_tokens pre-sizes a session (vllm_shift_connector.py:168-178)."""
+    from marathon_amd import BlockShiftStore, ShiftStore
+    from marathon_amd.connector import store_from_config
+
+    monkeypatch.delenv("MARATHON_STORE_TOKENS", raising=False)
+    st = store_from_config(None, worker=False)
+    assert isinstance(st, ShiftStore) and st.budget == 32768 and not st.allocate
+    monkeypatch.setenv("MARATHON_STORE_TOKENS", "5000")
+    assert store_from_config({}, worker=True).budget == 5000
+    st = store_from_config({"store_tokens": 7000, "store_device": "cpu",
+                            "session_tokens": 3000}, worker=True)
+    assert (st.budget, st.device, st.allocate, st.session_cap) == (7000, "cpu", True, 3000)
+    bst = store_from_config({"store_tokens": 640}, worker=True, block_layout=True)
+    assert isinstance(bst, BlockShiftStore) and bst.budget == 640 and bst.pool_blocks == 40
