@@ -410,6 +410,151 @@ class ShiftLoader:
                     entry["max_rel"], entry["mean_abs"])
 
 
+@dataclass
+class StepMeta:
+    """What the scheduler hands the worker for one engine step: the step's loads, then
+    its saves (the reference's ShiftConnectorMetadata, vllm_shift_connector.py:143-156)."""
+
+    loads: list
+    saves: list
+
+
+class ShiftScheduler:
+    """The connector's scheduler half over plain values (vllm_shift_connector.py:211-389).
+
+    A request's ``kv_transfer_params`` (``{"session", "load": {dst_start, dst_end,
+    delta}, "save": True | "full"}``, :16-18) come in; each engine step's
+    :class:`StepMeta` goes out, for :class:`ShiftLoader` and :class:`ShiftSaver`.  The
+    decisions are the reference's: one in-flight writer per session (:211-223);
+    ``plan_load`` against the scheduler's store (:247-288); a load issued once, in the
+    request's first scheduled step (:332-355); a save planned in every step, the
+    one-shot ``"full"`` widening to ``[0, hi)`` then downgraded (:296-330).  ``store``
+    is the scheduler's tensor-free mirror (``allocate=False``) of the worker's store:
+    both reach the same decisions from the same calls.
+
+    Loads and saves carry the request's block table (device-side slots,
+    :meth:`Load.from_blocks`), or host slot lists with ``device_slots=False``, as the
+    reference builds them.  The multi-segment ``"loads"`` path needs vLLM's gap-fill
+    patch (:247-271) and is not wired here; :func:`accept_multi` is its alignment.
+    """
+
+    def __init__(self, store, block_size: int, *, device_slots: bool = True):
+        from .shift_store import SessionTable
+
+        self.store = store
+        self.block_size = int(block_size)
+        self.device_slots = bool(device_slots)
+        self.table = SessionTable()
+        self._params: dict[str, dict] = {}
+        self._plans: dict[str, tuple] = {}
+        self._blocks: dict[str, list] = {}
+        self._need_load: set[str] = set()
+        self._step_tables: dict[str, np.ndarray] = {}
+        self.declines: list[str] = []
+
+    def on_new_request(self, rid: str, params: dict | None) -> None:
+        """Record the request's params; take the session's single writer slot."""
+        params = dict(params or {})
+        self._params[rid] = params
+        session = params.get("session")
+        if session and not self.table.acquire(rid, str(session)):
+            logger.warning("shift: session %s already has an in-flight writer; request %s "
+                           "runs with no reuse", session, rid)
+
+    def get_num_new_matched_tokens(self, rid: str, num_computed: int,
+                                   num_prompt_tokens: int) -> tuple[int, bool]:
+        """Tokens the store will provide past the local prefix hit (``plan_load``)."""
+        from .shift_store import plan_load
+
+        session = self.table.session_of(rid)
+        params = self._params.get(rid) or {}
+        req = params.get("load")
+        decision, why = plan_load(self.store, session, req, num_computed, num_prompt_tokens,
+                                  self.block_size)
+        if decision is None:
+            if session and req:
+                self.declines.append(why)
+                logger.warning("shift: session %s declining reuse: %s", session, why)
+            return 0, False
+        self._plans[rid] = (decision.lo, decision.hi, decision.delta)
+        return decision.hi - decision.lo, False
+
+    def update_state_after_alloc(self, rid: str, num_external_tokens: int) -> None:
+        if num_external_tokens > 0:
+            self._need_load.add(rid)
+
+    def _table_of(self, rid: str):
+        """The request's block table as of this step, one object per request per step:
+        a step's load and saves of one request then share one device table."""
+        tab = self._step_tables.get(rid)
+        if tab is None:
+            tab = self._step_tables[rid] = np.asarray(self._blocks[rid], np.int32)
+        return tab
+
+    def _load(self, rid: str, lo: int, hi: int, delta: int) -> Load:
+        session = self.table.session_of(rid) or ""
+        if self.device_slots:
+            return Load.from_blocks(session, self._table_of(rid), lo, hi, delta)
+        return Load(session, host_slots(self._blocks[rid], lo, hi, self.block_size), lo - delta,
+                    delta)
+
+    def _plan_save(self, meta: StepMeta, rid: str, lo: int, hi: int) -> None:
+        from .shift_store import plan_save
+
+        session = self.table.session_of(rid)
+        blocks = self._blocks.get(rid)
+        if not blocks:
+            return
+        params = self._params.get(rid) or {}
+        window = plan_save(self.store, session, params.get("save"), lo, hi)
+        if window is None:
+            if session and params.get("save") and hi > lo:
+                logger.warning("shift: session %s refused save of [%d,%d)", session, lo, hi)
+            return
+        if params.get("save") == "full":
+            params["save"] = True  # one-shot: the next steps save incrementally
+        lo, hi = window
+        if self.device_slots:
+            meta.saves.append(Save.from_blocks(session or "", self._table_of(rid), lo, hi))
+        else:
+            meta.saves.append(Save(session or "", host_slots(blocks, lo, hi, self.block_size),
+                                   lo))
+
+    def build_connector_meta(self, new_reqs=(), cached_reqs=(), finished=()) -> StepMeta:
+        """One engine step.  ``new_reqs``: ``(rid, block_ids, num_computed_tokens,
+        num_scheduled_tokens)`` of requests scheduled for the first time;
+        ``cached_reqs``: ``(rid, new_block_ids or None, num_computed_tokens,
+        num_scheduled_tokens)``; ``finished``: request ids to forget."""
+        meta = StepMeta([], [])
+        self._step_tables = {}
+        for rid, block_ids, computed, scheduled in new_reqs:
+            self._blocks[rid] = list(block_ids)
+            if rid in self._need_load:
+                lo, hi, delta = self._plans[rid]
+                meta.loads.append(self._load(rid, lo, hi, delta))
+                self._need_load.discard(rid)
+            self._plan_save(meta, rid, computed, computed + scheduled)
+        for rid, new_blocks, computed, scheduled in cached_reqs:
+            if new_blocks is not None:
+                self._blocks.setdefault(rid, []).extend(new_blocks)
+            self._plan_save(meta, rid, computed, computed + scheduled)
+        for rid in finished:
+            self._forget(rid)
+        return meta
+
+    def request_finished(self, rid: str) -> None:
+        """Forget the request and free its session's writer slot (:385-389)."""
+        self._forget(rid)
+        logger.info("shift: store %s", self.store.stats())
+
+    def _forget(self, rid: str) -> None:
+        self._blocks.pop(rid, None)
+        self._params.pop(rid, None)
+        self._plans.pop(rid, None)
+        self._need_load.discard(rid)
+        self.table.release(rid)
+
+
 class ShiftSaver:
     """Save path: paged cache -> session store, gathered on the device.
 

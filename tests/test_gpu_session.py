@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from marathon_amd import BlockShiftStore, ShiftStore, plan_load, plan_save, slots
-from marathon_amd.connector import Load, Save, ShiftLoader, ShiftSaver
+from marathon_amd.connector import Load, Save, ShiftLoader, ShiftSaver, ShiftScheduler
 from marathon_amd.shift_kernels import inv_freq_for
 
 pytestmark = pytest.mark.gpu
@@ -151,6 +151,82 @@ class RealKVEngine:
         torch.cuda.synchronize(self.dev)
 
 
+class ScheduledKVEngine(RealKVEngine):
+    """The same engine with every decision taken by ``ShiftScheduler``, the connector's
+    scheduler half, over a tensor-free mirror of the worker's store: the engine only
+    reports what vLLM's scheduler would (prefix hit, blocks, tokens per step), and the
+    worker runs each step's loads before the forward and its saves after it."""
+
+    def __init__(self, dev, store="flat", device_slots=False, **kw):
+        super().__init__(dev, store=store, device_slots=device_slots, **kw)
+        if store == "flat":
+            mirror = ShiftStore(budget_tokens=1 << 16, allocate=False, slab=1024)
+        else:
+            mirror = BlockShiftStore(budget_tokens=1 << 14, allocate=False, block_size=BS)
+        self.sched = ShiftScheduler(mirror, BS, device_slots=device_slots)
+        self.n_req = 0
+
+    @staticmethod
+    def _paged(item, lo):
+        if item.slots is not None:
+            return item.slots
+        return slots(list(item.block_ids), lo, lo + item.n, BS)
+
+    def _run_loads(self, meta):
+        if not meta.loads:
+            return
+        assert self.loader.start_load_kv(meta.loads) == sum(ld.n for ld in meta.loads) * LAYERS
+        for ld in meta.loads:
+            sl = self._paged(ld, ld.src_start + ld.delta)
+            st = self.store_shifts[ld.session]
+            self.shifts[sl] = st[ld.src_start:ld.src_start + ld.n] + int(ld.delta != 0)
+            self.loads += 1
+
+    def _run_saves(self, meta):
+        if not meta.saves:
+            return
+        assert self.saver.save_all(self.kv, meta.saves) == sum(sv.n for sv in meta.saves) * LAYERS
+        for sv in meta.saves:
+            sl = self._paged(sv, sv.dst_start)
+            st = self.store_shifts.setdefault(sv.session, torch.zeros(1 << 16, dtype=torch.int32))
+            st[sv.dst_start:sv.dst_start + sv.n] = self.shifts[sl]
+
+    def generate(self, ids, session, max_tokens, load=None, save=False):
+        rid = f"req{self.n_req}"
+        self.n_req += 1
+        blocks, hit = self._blocks_for(ids)
+        self.sched.on_new_request(rid, {"session": session, "load": load, "save": save})
+        ext, _ = self.sched.get_num_new_matched_tokens(rid, hit, len(ids))
+        self.sched.update_state_after_alloc(rid, ext)
+        computed = hit + ext
+        meta = self.sched.build_connector_meta(new_reqs=[(rid, blocks, computed,
+                                                          len(ids) - computed)])
+        assert len(meta.loads) == int(ext > 0)
+        self._run_loads(meta)
+        self._write_fresh(blocks, ids, computed, len(ids))
+        torch.cuda.synchronize(self.dev)
+        self._verify(blocks, ids)
+        self._run_saves(meta)
+        cur_ids = list(ids)
+        for _ in range(max_tokens):
+            cur = len(cur_ids)
+            new = None
+            if cur // BS >= len(blocks):
+                new = [self.next_block]
+                blocks.append(self.next_block)
+                self.next_block += 1
+            meta = self.sched.build_connector_meta(cached_reqs=[(rid, new, cur, 1)])
+            assert not meta.loads
+            cur_ids.append(1)
+            self._write_fresh(blocks, cur_ids, cur, cur + 1)
+            self._run_saves(meta)
+        self.sched.request_finished(rid)
+        for k in range(len(ids) // BS):
+            self.prefix.setdefault(tuple(ids[: (k + 1) * BS]), blocks[k])
+        torch.cuda.synchronize(self.dev)
+        self.declines = self.sched.declines
+
+
 def _prompt(messages):
     pieces = [list(f"{m['role']}: {m['content']}\n".encode()) for m in messages]
     return [i for p in pieces for i in p] + [10], pieces
@@ -165,14 +241,19 @@ def _phases(load, n_prompt):
     return [(lo, None), (n_prompt, {"dst_start": lo, "dst_end": hi, "delta": load["delta"]})]
 
 
-@pytest.mark.parametrize("store,device_slots", [
-    ("flat", False), ("flat", True), ("blocks", False), ("blocks", True)])
-def test_front_edits_through_the_real_kernels(gpu, store, device_slots):
-    eng = RealKVEngine(gpu, store=store, device_slots=device_slots)
+@pytest.mark.parametrize("store,device_slots,engine", [
+    ("flat", False, RealKVEngine), ("flat", True, RealKVEngine),
+    ("blocks", False, RealKVEngine), ("blocks", True, RealKVEngine),
+    ("flat", False, ScheduledKVEngine), ("blocks", True, ScheduledKVEngine)])
+def test_front_edits_through_the_real_kernels(gpu, store, device_slots, engine):
+    """``ScheduledKVEngine`` takes every decision through the connector's scheduler
+    half; the others call the planners directly."""
+    eng = engine(gpu, store=store, device_slots=device_slots)
     messages, keep_last, turns = [], 3, 9
     prompt_pieces = None  # pieces of the previous request's prompt: what the store holds
     for t in range(turns):
-        print(f"case session store={store} device_slots={device_slots} turn {t}", flush=True)
+        print(f"case session {engine.__name__} store={store} device_slots={device_slots} "
+              f"turn {t}", flush=True)
         load = None
         if t >= keep_last:
             d = t - keep_last
