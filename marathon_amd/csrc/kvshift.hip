@@ -667,15 +667,26 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
           sbv[u] = sbv[0];
           dbk[u] = dbk[0];
           dbv[u] = dbv[0];
+        } else if (UNIFORM) {
+          sbk[u] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb));
+          sbv[u] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb));
+          dbk[u] = reinterpret_cast<char*>(ld_const(p.dst_k_base + db));
+          dbv[u] = reinterpret_cast<char*>(ld_const(p.dst_v_base + db));
         } else {
-          sbk[u] = reinterpret_cast<const char*>(UNIFORM ? ld_const(p.src_k_base + sb)
-                                                         : p.src_k_base[sb]);
-          sbv[u] = reinterpret_cast<const char*>(UNIFORM ? ld_const(p.src_v_base + sb)
-                                                         : p.src_v_base[sb]);
-          dbk[u] = reinterpret_cast<char*>(UNIFORM ? ld_const(p.dst_k_base + db)
-                                                   : p.dst_k_base[db]);
-          dbv[u] = reinterpret_cast<char*>(UNIFORM ? ld_const(p.dst_v_base + db)
-                                                   : p.dst_v_base[db]);
+          // rows of several tokens: they usually share one (group, layer) base row,
+          // read with scalar loads (a per-lane gather measured 6-10% slower); the
+          // gather runs only when the wave straddles groups
+          const int sb0 = uniform(sb), db0 = uniform(db);
+          sbk[u] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb0));
+          sbv[u] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb0));
+          dbk[u] = reinterpret_cast<char*>(ld_const(p.dst_k_base + db0));
+          dbv[u] = reinterpret_cast<char*>(ld_const(p.dst_v_base + db0));
+          if (!__all(sb == sb0 && db == db0)) {
+            sbk[u] = reinterpret_cast<const char*>(p.src_k_base[sb]);
+            sbv[u] = reinterpret_cast<const char*>(p.src_v_base[sb]);
+            dbk[u] = reinterpret_cast<char*>(p.dst_k_base[db]);
+            dbv[u] = reinterpret_cast<char*>(p.dst_v_base[db]);
+          }
         }
         live[u] = live[u] && span_u[u] >= 0;
         const bool aligned =

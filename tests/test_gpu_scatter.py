@@ -155,6 +155,42 @@ def test_geometry_limits(gpu, dtype, heads, d, rotary, hnd):
     assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
 
 
+@pytest.mark.parametrize("dtype,heads,d,rotary,hnd", [
+    (torch.bfloat16, 1, 128, 128, True),       # 4 tokens per wave pass
+    (torch.bfloat16, 2, 128, 128, False),      # 2 tokens per pass
+    (torch.bfloat16, 1, 64, 64, False),        # 8 tokens per pass
+    (torch.bfloat16, 2, 64, 32, True),         # 4 tokens per pass, partial rotary
+    (torch.float16, 2, 128, 128, True),
+    (torch.float32, 1, 128, 64, False),        # fp32: 2 rows per wave, 2 tokens
+    (torch.float8_e4m3fn, 1, 128, 128, True),  # fp8: 8 tokens per pass
+    (torch.float8_e4m3fn, 2, 128, 64, False),  # fp8: 4 tokens per pass, partial rotary
+    (torch.float8_e4m3fn, 4, 128, 128, True),  # fp8: 2 tokens per pass
+])
+@pytest.mark.parametrize("n", [37, 300])
+def test_multi_token_passes(gpu, dtype, heads, d, rotary, hnd, n):
+    """Head counts that divide a wave's rows: a wave pass covers several whole tokens.
+    Ragged tails (37 and 300 tokens are not multiples of any tile) and every element
+    type, against the oracle."""
+    print(f"case multi-token {dtype} heads={heads} d={d} rotary={rotary} hnd={hnd} n={n}",
+          flush=True)
+    g = torch.Generator().manual_seed(heads * 7919 + d + rotary + n)
+    scale, nblocks, delta = 0.05, 24, 1187
+    src = randn((n, heads, 2 * d), dtype, g, scale)
+    shape = (nblocks, heads, 16, 2 * d) if hnd else (nblocks, 16, heads, 2 * d)
+    kv = randn(shape, dtype, g, scale)
+    table = torch.randperm(nblocks, generator=g)
+    pos = torch.arange(9, 9 + n)
+    slots = table[pos // 16] * 16 + pos % 16
+    inv = inv_freq(rotary)
+    fp8 = dtype == torch.float8_e4m3fn
+    got = bits(_run_gpu(gpu, src, kv, slots, 16, hnd, rope_shift(delta, d, inv, gpu),
+                        **({"k_scale": scale} if fp8 else {})))
+    want = bits(kv)
+    orc.scatter_shifted(bits(src), want, slots.numpy(), 16, hnd, delta, inv.numpy(),
+                        dname(dtype), **({"k_scale": np.float32(scale)} if fp8 else {}))
+    assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
+
+
 def test_source_view_into_a_store_buffer(gpu):
     """The connector hands the kernel ``buf[start:start+n]`` of a store buffer."""
     g = torch.Generator().manual_seed(3)

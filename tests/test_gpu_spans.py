@@ -177,14 +177,52 @@ def test_batched_other_geometries_match_oracle(gpu, dtype, heads, d, rotary):
         assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
 
 
-def test_out_of_range_rows_are_flagged_and_skipped(gpu):
+@pytest.mark.parametrize("dtype,heads,d,rotary", [
+    (torch.bfloat16, 1, 128, 128),       # 4 tokens per wave pass
+    (torch.bfloat16, 2, 128, 128),       # 2 tokens per pass
+    (torch.bfloat16, 1, 64, 64),         # 8 tokens per pass
+    (torch.bfloat16, 4, 64, 32),         # 2 tokens per pass, partial rotary
+    (torch.float16, 1, 128, 128),
+    (torch.float32, 1, 128, 128),        # fp32: 2 tokens per pass
+    (torch.float8_e4m3fn, 1, 128, 128),  # fp8: 8 tokens per pass
+    (torch.float8_e4m3fn, 2, 128, 128),  # fp8: 4 tokens per pass
+    (torch.float8_e4m3fn, 4, 128, 64),   # fp8: 2 tokens per pass, partial rotary
+])
+def test_batched_multi_token_passes_match_oracle(gpu, dtype, heads, d, rotary):
+    """Head counts that divide a wave's rows: a wave pass covers several whole tokens.
+    Span boundaries fall at odd tokens, so passes straddle spans of different deltas and
+    the two sessions (base-address rows of different groups, the per-lane fallback);
+    every destination byte against the oracle."""
+    print(f"case batched multi-token {dtype} heads={heads} d={d} rotary={rotary}", flush=True)
+    table = torch.randperm(48, generator=torch.Generator().manual_seed(4)).tolist()
+    spans = [(5, 3, 0, 0, 121, -41, 0, 0),
+             (150, 130, 0, 0, 138, 1999, 0, 0),  # session 1 starts at token 259
+             (0, 300, 0, 0, 191, 0, 1, 0),     # session 1, delta 0: a plain copy
+             (17, 520, 0, 0, 179, -7, 1, 0)]
+    k_scale = torch.tensor([0.044, 0.072]) if dtype == torch.float8_e4m3fn else None
+    plan, kv = _two_session_plan(gpu, dtype, heads, d, rotary, 13, spans, table, k_scale)
+    src_o = oracle_side(plan.src, "flat", None)
+    dst_o = oracle_side(plan.dst, "table", torch.tensor(table, dtype=torch.int32))
+    orc.shift_spans(oracle_spans(span_array(spans)), src_o, dst_o, inv_freq(rotary).numpy(),
+                    dname(dtype), None if k_scale is None else k_scale.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer, t in enumerate(kv):
+        assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
+
+
+@pytest.mark.parametrize("heads", [8, 2, 1])
+def test_out_of_range_rows_are_flagged_and_skipped(gpu, heads):
     """Bad indices on either side never write: a -1 and a too-large block id in the
     destination table, source positions past a session's rows, and a span naming a
     group that does not exist.  Each raises its flag; every other row lands exactly as
-    in a plan that leaves the bad rows out."""
+    in a plan that leaves the bad rows out.  8 heads: one token per wave pass; 2 and 1:
+    several tokens per pass, good and bad ones side by side."""
     from marathon_amd import _lib
 
-    print("case out-of-range rows", flush=True)
+    print(f"case out-of-range rows heads={heads}", flush=True)
     table = torch.randperm(48, generator=torch.Generator().manual_seed(5)).tolist()
     bad_table = list(table)
     bad_table[2] = -1  # positions 32..47
@@ -196,10 +234,10 @@ def test_out_of_range_rows_are_flagged_and_skipped(gpu):
                 (28, 48, 0, 0, 16, 33, 0, 0),       # 48..64
                 (60, 80, 0, 0, 20, 33, 0, 0),       # 80..100
                 (190, 400, 0, 0, 10, -5, 1, 0)]     # src 190..200
-    fill = torch.full((48, 8, 16, 256), 3.0).to(torch.bfloat16)
-    plan_b, kv_b = _two_session_plan(gpu, torch.bfloat16, 8, 128, 128, 4, spans_bad,
+    fill = torch.full((48, heads, 16, 256), 3.0).to(torch.bfloat16)
+    plan_b, kv_b = _two_session_plan(gpu, torch.bfloat16, heads, 128, 128, 4, spans_bad,
                                      bad_table, fill=fill)
-    plan_g, kv_g = _two_session_plan(gpu, torch.bfloat16, 8, 128, 128, 4, spans_ok, table,
+    plan_g, kv_g = _two_session_plan(gpu, torch.bfloat16, heads, 128, 128, 4, spans_ok, table,
                                      fill=fill)
     fb = torch.zeros(1, dtype=torch.int32, device=gpu)
     fg = torch.zeros(1, dtype=torch.int32, device=gpu)
@@ -213,13 +251,14 @@ def test_out_of_range_rows_are_flagged_and_skipped(gpu):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_single_span_out_of_range_slot_is_flagged_and_skipped(gpu):
+@pytest.mark.parametrize("heads", [8, 1])
+def test_single_span_out_of_range_slot_is_flagged_and_skipped(gpu, heads):
     from marathon_amd import _lib, rope_shift, scatter_shifted
 
-    print("case single-span out-of-range slot", flush=True)
+    print(f"case single-span out-of-range slot heads={heads}", flush=True)
     g = torch.Generator().manual_seed(8)
-    src = torch.randn(40, 8, 256, generator=g).to(torch.bfloat16).to(gpu)
-    kv = torch.zeros(4, 8, 16, 256, dtype=torch.bfloat16, device=gpu)
+    src = torch.randn(40, heads, 256, generator=g).to(torch.bfloat16).to(gpu)
+    kv = torch.zeros(4, heads, 16, 256, dtype=torch.bfloat16, device=gpu)
     kv_ok = kv.clone()
     sl = torch.arange(40, dtype=torch.int64)
     sl[7] = 64  # the cache holds 64 slots
