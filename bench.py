@@ -22,6 +22,8 @@ Prints one JSON line.  Also measured, in the same line:
 * ``reference_loop``: the reference benchmark's own loop through the drop-in API: 40
   per-layer ``scatter_shifted`` calls per shift at 4,096, 12,288 and 30,720 tokens, the
   rows of its published table.
+* ``tp_shares``: the headline shift at 4, 2 and 1 KV heads (one GPU's share at TP 2, 4,
+  8), bf16 and fp8.
 """
 
 from __future__ import annotations
@@ -311,6 +313,40 @@ def other_workloads(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def tp_shares(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: one GPU's share of the headline shift under tensor parallelism
+    over KV heads (4, 2 and 1 heads of 8), bf16 and fp8, one launch per step."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+
+    out = {}
+    for heads in (4, 2, 1):
+        for name, make in (("bf16", lambda h: W.qwen3_14b_multispan(dev, heads=h)),
+                           ("fp8", lambda h: W.qwen3_14b_multispan_fp8(dev, heads=h))):
+            wl = make(heads)
+            plan = wl.plan()
+            # these shifts take 0.1-0.7 ms: launch for a quarter second first, so the
+            # timed launches do not start on an idle, down-clocked GPU
+            t_end = time.perf_counter() + 0.25
+            while time.perf_counter() < t_end:
+                for _ in range(10):
+                    plan.launch(stream.cuda_stream)
+                torch.cuda.synchronize()
+            _, per = time_plan(plan, max(steps, 50), warmup, stream)
+            ms = float(np.median(per))
+            gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+            row = {"heads": heads, "ms": round(ms, 4), "GB_s": round(gbs, 1),
+                   "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+            if name == "bf16":
+                row["rows_checked"] = spot_check(wl, rows=32, seed=heads)
+            out[f"tp{8 // heads}_{name}"] = row
+            del wl, plan
+            torch.cuda.empty_cache()
+    return out
+
+
 def connector_step(dev, steps: int, warmup: int) -> dict:
     """Worker load steps through the connector: a session held in the block-layout store,
     loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
@@ -475,6 +511,8 @@ def main() -> int:
                     action="store_true",
                     help="skip the informational timings of the Qwen3-8B single-span, fp8 "
                     "multi-span and batched-session workloads")
+    ap.add_argument("--no-tp-shares", action="store_true",
+                    help="skip the timings of one GPU's share at 4, 2 and 1 KV heads")
     ap.add_argument("--no-connector-step", action="store_true",
                     help="skip the end-to-end connector load and save step timings")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -540,6 +578,9 @@ def main() -> int:
     if not args.no_other_workloads:
         extra["other_workloads"] = other_workloads(dev, side_steps, args.warmup,
                                                    stream)
+    if not args.no_tp_shares:
+        log("tensor-parallel shares of the headline shift (4, 2, 1 KV heads)")
+        extra["tp_shares"] = tp_shares(dev, side_steps, args.warmup, stream)
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
         extra["connector_step"] = connector_step(dev, side_steps, args.warmup)

@@ -171,7 +171,7 @@ class Workload:
     @property
     def algorithmic_bytes(self) -> int:
         eb = self.dst.first.element_size()
-        return 2 * self.tokens * self.layers * HEADS * 2 * HEAD_SIZE * eb
+        return 2 * self.tokens * self.layers * self.dst.heads * 2 * self.dst.head_size * eb
 
 
 def _randn_cache(shape, dtype, gen, device, scale=None) -> torch.Tensor:
@@ -182,8 +182,8 @@ def _randn_cache(shape, dtype, gen, device, scale=None) -> torch.Tensor:
     return torch.randn(shape, dtype=dtype, device=device, generator=gen)
 
 
-def _paged(blocks, layout):
-    return (blocks, HEADS, BLOCK, 2 * HEAD_SIZE) if layout == "hnd" else (blocks, BLOCK, HEADS, 2 * HEAD_SIZE)
+def _paged(blocks, layout, heads=HEADS):
+    return (blocks, heads, BLOCK, 2 * HEAD_SIZE) if layout == "hnd" else (blocks, BLOCK, heads, 2 * HEAD_SIZE)
 
 
 def single_session_workload(
@@ -197,9 +197,11 @@ def single_session_workload(
     scale_seed: int | None = None,
     spare_blocks: int = 64,
     dst_fill: str = "zeros",
+    heads: int = HEADS,
 ) -> Workload:
     """One session's store (NHD blocks via a shuffled table) -> one HND paged cache via
-    a slot mapping: the single-span and multi-span workloads, bf16 or fp8."""
+    a slot mapping: the single-span and multi-span workloads, bf16 or fp8.  ``heads``
+    below 8 is one GPU's share of the KV heads under tensor parallelism."""
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -216,17 +218,18 @@ def single_session_workload(
     src_caches, dst_caches = [], []
     for layer in range(layers):
         if dtype == torch.float8_e4m3fn:
-            kk = _randn_cache(_paged(src_blocks, "nhd")[:-1] + (HEAD_SIZE,), dtype, gen, device,
-                              k_scale[layer])
-            vv = _randn_cache(_paged(src_blocks, "nhd")[:-1] + (HEAD_SIZE,), dtype, gen, device,
-                              v_scale[layer])
+            kk = _randn_cache(_paged(src_blocks, "nhd", heads)[:-1] + (HEAD_SIZE,), dtype, gen,
+                              device, k_scale[layer])
+            vv = _randn_cache(_paged(src_blocks, "nhd", heads)[:-1] + (HEAD_SIZE,), dtype, gen,
+                              device, v_scale[layer])
             src_caches.append(torch.cat((kk, vv), dim=-1))
         else:
-            src_caches.append(_randn_cache(_paged(src_blocks, "nhd"), dtype, gen, device))
+            src_caches.append(_randn_cache(_paged(src_blocks, "nhd", heads), dtype, gen, device))
         if dst_fill == "random" and dtype != torch.float8_e4m3fn:
-            dst_caches.append(_randn_cache(_paged(dst_pool, "hnd"), dtype, gen, device))
+            dst_caches.append(_randn_cache(_paged(dst_pool, "hnd", heads), dtype, gen, device))
         else:
-            dst_caches.append(torch.zeros(_paged(dst_pool, "hnd"), dtype=dtype, device=device))
+            dst_caches.append(torch.zeros(_paged(dst_pool, "hnd", heads), dtype=dtype,
+                                          device=device))
     dst_slots, rows, off = [], [], 0
     for s, d, n, dl in zip(layout.src_start, layout.dst_start, layout.length, layout.delta):
         dst_slots.append(slot_map(dst_table, int(d), int(d + n), BLOCK))
