@@ -46,6 +46,18 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def warm_up(launch, seconds: float = 0.25) -> None:
+    """Launch repeatedly for ``seconds`` (the side sections' shifts take 0.1-12 ms;
+    timed straight after building a workload, the first launches run on an idle GPU and
+    read up to 12% slow)."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        launch()
+        torch.cuda.synchronize()
+
+
 def time_plan(plan, steps: int, warmup: int, stream):
     import torch
 
@@ -205,6 +217,7 @@ def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
     plan = ShiftPlan(span_array([(0, 0, 0, 0, n, 186, 0, 0)]), CacheSet([src], "flat"),
                      CacheSet([kv], "hnd", bs), inv_freq=inv_freq_for(d, 1e6),
                      src_mode="flat", dst_mode="slots", dst_index=slot)
+    warm_up(lambda: plan.launch(stream.cuda_stream))
     wall, per = time_plan(plan, steps, warmup, stream)
     ms = float(np.mean(per))
     out = {
@@ -224,7 +237,7 @@ def reference_loop(dev, iters: int = 5) -> dict:
     (scripts/bench_shift_copy.py:24-53): for each of 40 layers, one ``scatter_shifted``
     call from a ``[n, 8, 256]`` bf16 store slice into an HND paged cache through a
     scattered slot mapping, delta 186.  Host wall clock around the 40 calls
-    (synchronised on both sides), best of ``iters`` passes after one warm-up; bytes are
+    (synchronised on both sides), best of ``iters`` passes after a warm-up; bytes are
     the source read once plus the destination written once.  One row per token count
     of its published table (docs/findings.md:644-646, RTX 5090)."""
     import numpy as np
@@ -238,7 +251,7 @@ def reference_loop(dev, iters: int = 5) -> dict:
     shift = rope_shift(186, d, inv, dev)
     published = {4096: 1.01, 12288: 2.80, 30720: 6.54}
     out = {"what": "40 per-layer scatter_shifted calls per shift (the reference's call "
-           "pattern), best of %d after 1 warm-up, host wall clock" % iters}
+           "pattern), best of %d after a 0.25 s warm-up, host wall clock" % iters}
     for n, ref_ms in published.items():
         gen = torch.Generator(device=dev)
         gen.manual_seed(n)
@@ -251,6 +264,12 @@ def reference_loop(dev, iters: int = 5) -> dict:
         pos = torch.arange(n, device=dev)
         slots = table[pos // bs] * bs + pos % bs
         best = host = float("inf")
+
+        def one_shift():
+            for s, k in zip(src, kv):
+                scatter_shifted(s, k, slots, bs, True, shift)
+
+        warm_up(one_shift)
         for i in range(iters + 1):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -298,6 +317,7 @@ def other_workloads(dev, steps: int, warmup: int, stream) -> dict:
         log(f"timing {name}")
         wl = make()
         plan = wl.plan()
+        warm_up(lambda: plan.launch(stream.cuda_stream))
         _, per = time_plan(plan, steps, warmup, stream)
         ms = float(np.mean(per))
         out[name] = {
@@ -327,13 +347,7 @@ def tp_shares(dev, steps: int, warmup: int, stream) -> dict:
                            ("fp8", lambda h: W.qwen3_14b_multispan_fp8(dev, heads=h))):
             wl = make(heads)
             plan = wl.plan()
-            # these shifts take 0.1-0.7 ms: launch for a quarter second first, so the
-            # timed launches do not start on an idle, down-clocked GPU
-            t_end = time.perf_counter() + 0.25
-            while time.perf_counter() < t_end:
-                for _ in range(10):
-                    plan.launch(stream.cuda_stream)
-                torch.cuda.synchronize()
+            warm_up(lambda: plan.launch(stream.cuda_stream))
             _, per = time_plan(plan, max(steps, 50), warmup, stream)
             ms = float(np.median(per))
             gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
