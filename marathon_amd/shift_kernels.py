@@ -136,6 +136,9 @@ def current_stream(device: torch.device) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -168,7 +171,7 @@ def scatter_shifted(
     current stream.  ``k_scale`` (fp8 caches only) is the layer's K scale;
     ``error_flags`` an optional int32 device tensor that collects out-of-range bits.
     """
-    if not use_hip(kv):
+    if not kv.is_cuda:
         raise RuntimeError(
             "scatter_shifted: kv is not on a HIP device; marathon_amd has no CPU path"
         )
@@ -179,12 +182,15 @@ def scatter_shifted(
         return
     if src.dtype != kv.dtype:
         raise TypeError(f"src dtype {src.dtype} != kv dtype {kv.dtype}")
-    if src.device != kv.device:
+    # device indices as ints: a per-layer call runs these checks 40 times per shift
+    dev = kv.get_device()
+    if src.get_device() != dev:
         raise ValueError(f"src on {src.device}, kv on {kv.device}")
-    if src.stride(2) != 1 or kv.stride(3) != 1:
+    ss, ks = src.stride(), kv.stride()
+    if ss[2] != 1 or ks[3] != 1:
         raise ValueError("src and kv rows must be contiguous in the last dimension")
     code = dtype_code(kv.dtype)
-    if slots.device != kv.device or slots.dtype != torch.int64 or not slots.is_contiguous():
+    if slots.get_device() != dev or slots.dtype != torch.int64 or not slots.is_contiguous():
         slots = slots.to(device=kv.device, dtype=torch.int64, non_blocking=True).contiguous()
     if slots.numel() != n:
         raise ValueError(f"{slots.numel()} slots for {n} tokens")
@@ -192,7 +198,7 @@ def scatter_shifted(
     cos = sgn = scale = None
     if rotate:
         cos, sgn = shift.cos, shift.sgn
-        if cos.device != kv.device:
+        if cos.get_device() != dev:
             cos, sgn = cos.to(kv.device), sgn.to(kv.device)
         if cos.numel() != d or sgn.numel() != d:
             raise ValueError(f"rotation tables of {cos.numel()} for head_size {d}")
@@ -200,11 +206,12 @@ def scatter_shifted(
             if k_scale is None:
                 raise ValueError("fp8 KV cache needs k_scale")
             scale = _scale_tensor(k_scale, kv.device)
-    blk_s, head_s, off_s = paged_strides(kv, hnd)
+    blk_s, head_s, off_s = (ks[0], ks[1], ks[2]) if hnd else (ks[0], ks[2], ks[1])
+    stream = _raw_stream(dev) if _raw_stream is not None else current_stream(kv.device)
     args = (
         src.data_ptr(),
-        src.stride(0),
-        src.stride(1),
+        ss[0],
+        ss[1],
         kv.data_ptr(),
         blk_s,
         head_s,
@@ -216,18 +223,18 @@ def scatter_shifted(
         d,
         int(block_size),
         code,
-        _ptr(cos),
-        _ptr(sgn),
+        None if cos is None else cos.data_ptr(),
+        None if sgn is None else sgn.data_ptr(),
         shift.rotary if rotate else 0,
-        _ptr(scale),
-        _ptr(error_flags),
-        ctypes.c_void_p(current_stream(kv.device)),
+        None if scale is None else scale.data_ptr(),
+        None if error_flags is None else error_flags.data_ptr(),
+        ctypes.c_void_p(int(stream)),
     )
     fn = _lib.lib().mkv_scatter_shifted
-    if kv.device.index == torch.cuda.current_device():
+    if dev == _current_device():
         rc = fn(*args)
     else:
-        with torch.cuda.device(kv.device):  # the launch goes to the current device
+        with torch.cuda.device(dev):  # the launch goes to the current device
             rc = fn(*args)
     _lib.check(rc)
 
