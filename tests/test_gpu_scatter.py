@@ -191,6 +191,19 @@ def test_multi_token_passes(gpu, dtype, heads, d, rotary, hnd, n):
     assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
 
 
+@pytest.mark.parametrize("delta", [131071, -1048577, 16777219, 2**31 - 1, -(2**31)])
+def test_extreme_deltas_match_oracle(gpu, delta):
+    """int32 extremes and deltas beyond 2^24 (rounded to fp32 before the product, as
+    torch rounds the reference's Python scalar): bit-exact against the oracle."""
+    print(f"case extreme delta={delta}", flush=True)
+    src, kv, slots = _case(abs(delta) % 1000, 53, True)
+    inv = inv_freq()
+    got = bits(_run_gpu(gpu, src, kv, slots, 16, True, rope_shift(delta, 128, inv, gpu)))
+    want = bits(kv)
+    orc.scatter_shifted(bits(src), want, slots.numpy(), 16, True, delta, inv.numpy(), "bf16")
+    assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
+
+
 def test_source_view_into_a_store_buffer(gpu):
     """The connector hands the kernel ``buf[start:start+n]`` of a store buffer."""
     g = torch.Generator().manual_seed(3)

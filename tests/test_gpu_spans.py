@@ -213,6 +213,31 @@ def test_batched_multi_token_passes_match_oracle(gpu, dtype, heads, d, rotary):
         assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_batched_extreme_deltas_match_oracle(gpu, dtype):
+    """The plan kernel evaluates each span's cos/sin on the device: int32 extremes and
+    deltas beyond 2^24, against the oracle byte for byte."""
+    print(f"case batched extreme deltas {dtype}", flush=True)
+    table = torch.randperm(48, generator=torch.Generator().manual_seed(6)).tolist()
+    spans = [(5, 3, 0, 0, 70, 2**31 - 1, 0, 0),
+             (90, 80, 0, 0, 61, -(2**31), 0, 0),
+             (0, 300, 0, 0, 45, 16777219, 1, 0),
+             (50, 400, 0, 0, 77, -1048577, 1, 0),
+             (130, 520, 0, 0, 33, 131071, 1, 0)]
+    k_scale = torch.tensor([0.05, 0.021]) if dtype == torch.float8_e4m3fn else None
+    plan, kv = _two_session_plan(gpu, dtype, 8, 128, 128, 21, spans, table, k_scale)
+    src_o = oracle_side(plan.src, "flat", None)
+    dst_o = oracle_side(plan.dst, "table", torch.tensor(table, dtype=torch.int32))
+    orc.shift_spans(oracle_spans(span_array(spans)), src_o, dst_o, inv_freq(128).numpy(),
+                    dname(dtype), None if k_scale is None else k_scale.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer, t in enumerate(kv):
+        assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
+
+
 @pytest.mark.parametrize("heads", [8, 2, 1])
 def test_out_of_range_rows_are_flagged_and_skipped(gpu, heads):
     """Bad indices on either side never write: a -1 and a too-large block id in the

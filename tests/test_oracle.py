@@ -18,6 +18,8 @@ from oracle import kvshift_oracle as orc
 from oracle import torch_path
 
 DELTAS = [-3000, -4, 0, 4, 186, 10000]
+# int32 extremes and deltas whose fp32 conversion rounds (beyond 2^24)
+EXTREME_DELTAS = [131071, -1048577, 16777219, -33554435, 2**31 - 1, -(2**31)]
 
 
 def _inv(rotary=128, theta=1e6):
@@ -42,9 +44,18 @@ def test_angles_are_one_fp32_rounding_of_the_exact_product():
         got = orc.angles(delta, inv)
         exact = np.float64(delta) * inv.astype(np.float64)  # exact: 24-bit x <=24-bit int
         assert np.array_equal(got, exact.astype(np.float32)), delta
+    # beyond 2^24 the delta itself is first rounded to fp32, as torch rounds the Python
+    # scalar of ``float(delta) * inv_freq`` to the tensor's fp32 (shift_kernels.py:73)
+    for delta in EXTREME_DELTAS:
+        d32 = np.float64(np.float32(delta))
+        assert d32 == float(torch.tensor(float(delta), dtype=torch.float32))
+        got = orc.angles(delta, inv)
+        assert np.array_equal(got, (d32 * inv.astype(np.float64)).astype(np.float32)), delta
+        want = (float(delta) * torch.from_numpy(inv)).numpy()
+        assert np.array_equal(got, want), delta
 
 
-@pytest.mark.parametrize("delta", DELTAS + [-566, 6759, -2048])
+@pytest.mark.parametrize("delta", DELTAS + [-566, 6759, -2048] + EXTREME_DELTAS)
 def test_cos_sin_are_correctly_rounded_and_agree_with_torch(delta):
     inv = _inv()
     c, s = orc.cos_sin(delta, inv, "cr")
@@ -164,7 +175,7 @@ def test_rerotation_is_invertible_composes_and_preserves_pair_norms():
     assert np.allclose(n0, n1, rtol=1e-6, atol=1e-6)
 
 
-@pytest.mark.parametrize("delta", DELTAS + [-566])
+@pytest.mark.parametrize("delta", DELTAS + [-566] + EXTREME_DELTAS)
 def test_bf16_rotation_is_the_reference_op_sequence(delta):
     """With torch's own CPU tables, the oracle's bit-level rotation equals the reference
     torch path's bytes exactly (same fp32 ops, same rounding)."""
