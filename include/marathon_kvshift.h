@@ -135,7 +135,8 @@ typedef struct mkv_side {
  *                  launch and the workspace); tokens beyond it are not moved and raise
  *                  MKV_FLAG_SPAN.
  *   inv_freq     : device fp32 [rotary / 2]; may be NULL when rotary == 0.
- *   k_scale      : device fp32 [layers], fp8 only (NULL otherwise).
+ *   k_scale      : device fp32 [layers] for MKV_FP8_E4M3 when rotary > 0; otherwise
+ *                  ignored and may be NULL (with rotary 0 every K byte is copied).
  *   error_flags  : device int32 [1] or NULL.
  *   workspace    : device, >= mkv_shift_workspace_size(total_tokens, n_spans, rotary)
  *                  bytes, 16-byte aligned; overwritten by every call, so calls that

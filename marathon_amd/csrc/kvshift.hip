@@ -603,7 +603,11 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       if (p.rotate) scale = ld_const(p.k_scale);
     }
   } else {
-    if constexpr (DT == MKV_FP8_E4M3) scale = ld_const(p.k_scale + layer);
+    // the scale dequantises K for the rotation; with rotary 0 nothing is rotated and
+    // k_scale may be NULL
+    if constexpr (DT == MKV_FP8_E4M3) {
+      if (p.rotary > 0) scale = ld_const(p.k_scale + layer);
+    }
   }
   const float rcp = 1.0f / scale;  // correctly rounded (fp8 requantisation)
 
@@ -1051,7 +1055,7 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
   if (d->spans == nullptr) return fail(MKV_ERR_ARG, "NULL span table");
   if (d->layers <= 0) return fail(MKV_ERR_ARG, "layers %d", d->layers);
   if (d->rotary > 0 && d->inv_freq == nullptr) return fail(MKV_ERR_ARG, "inv_freq is NULL");
-  if (d->dtype == MKV_FP8_E4M3 && d->k_scale == nullptr)
+  if (d->dtype == MKV_FP8_E4M3 && d->rotary > 0 && d->k_scale == nullptr)
     return fail(MKV_ERR_ARG, "fp8 needs k_scale");
   if (d->src.k_base == nullptr || d->src.v_base == nullptr || d->dst.k_base == nullptr ||
       d->dst.v_base == nullptr)

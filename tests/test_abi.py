@@ -145,6 +145,11 @@ def test_batched_entry_point_argument_errors_need_no_gpu():
     d.src.mode = 7
     assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
     assert b"mode" in lib.mkv_last_error()
+    # fp8 needs the layers' K scales only when it rotates (the check precedes any launch)
+    d.src.mode = _lib.MKV_ADDR_FLAT
+    d.dtype, d.k_scale = _lib.MKV_FP8_E4M3, None
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    assert b"k_scale" in lib.mkv_last_error()
 
 
 def test_python_api_refuses_tensors_off_the_gpu():

@@ -1,0 +1,147 @@
+"""Seeded random batched shifts against the oracle, byte for byte.
+
+Each case draws a geometry (element type, head size, heads, rotary width, layers, block
+size), a source side (flat session stores, or paged NHD / HND caches through block
+tables, one to three groups), a destination side (a paged NHD or HND cache through a
+slot mapping or a block table, one or two groups) and one to six spans with disjoint
+destinations and deltas of both signs, zero and large.  Every destination byte of every
+layer must equal the oracle's, and no error flag may be raised.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from marathon_amd.spans import CacheSet, ShiftPlan, span_array
+from oracle import kvshift_oracle as orc
+from tests.helpers import bits, dname, inv_freq, oracle_side, oracle_spans, randn
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float16, torch.float32, torch.float8_e4m3fn]
+EB = {torch.bfloat16: 2, torch.float16: 2, torch.float32: 4, torch.float8_e4m3fn: 1}
+
+
+def _case(seed: int):
+    rng = np.random.default_rng(seed)
+    dtype = DTYPES[seed % len(DTYPES)]
+    eb = EB[dtype]
+    d = int(rng.choice([64, 128, 256]))
+    per_chunk = 16 // eb
+    rot_choices = [r for r in (0, d // 2, d) if r % (2 * per_chunk) == 0]
+    rotary = int(rng.choice(rot_choices))
+    heads = int(rng.choice([1, 2, 3, 4, 5, 6, 8, 12, 16]))
+    layers = int(rng.integers(1, 4))
+    bs = int(rng.choice([16, 16, 32]))
+    src_layout = str(rng.choice(["flat", "nhd", "hnd"]))
+    dst_layout = str(rng.choice(["nhd", "hnd"]))
+    dst_mode = str(rng.choice(["slots", "table"]))
+    src_groups = int(rng.integers(1, 4))
+    dst_groups = int(rng.integers(1, 3)) if dst_mode == "table" else 1
+    return dict(seed=seed, dtype=dtype, d=d, rotary=rotary, heads=heads, layers=layers,
+                bs=bs, src_layout=src_layout, dst_layout=dst_layout, dst_mode=dst_mode,
+                src_groups=src_groups, dst_groups=dst_groups, rng=rng)
+
+
+def _paged_shape(blocks, layout, bs, heads, d):
+    return (blocks, heads, bs, 2 * d) if layout == "hnd" else (blocks, bs, heads, 2 * d)
+
+
+def _build(c, gpu):
+    rng, dtype, d, heads, layers, bs = c["rng"], c["dtype"], c["d"], c["heads"], c["layers"], c["bs"]
+    gen = torch.Generator().manual_seed(c["seed"])
+    fp8 = dtype == torch.float8_e4m3fn
+    sc = 0.05
+
+    # source: per group, a flat store of `rows` positions or a paged cache through a table
+    src_rows = [int(rng.integers(64, 400)) for _ in range(c["src_groups"])]
+    src_caches, src_tabs, src_tab_off = [], [], []
+    if c["src_layout"] == "flat":
+        for g in range(c["src_groups"]):
+            src_caches.append([randn((src_rows[g], heads, 2 * d), dtype, gen, sc)
+                               for _ in range(layers)])
+    else:
+        # one block count for every group (a CacheSet's groups share trailing shapes;
+        # the block count may differ, but equal sizes keep the case simple)
+        nb = max(-(-r // bs) for r in src_rows) + 2
+        off = 0
+        for g in range(c["src_groups"]):
+            src_caches.append([randn(_paged_shape(nb, c["src_layout"], bs, heads, d), dtype,
+                                     gen, sc) for _ in range(layers)])
+            src_tabs.append(rng.permutation(nb)[: -(-src_rows[g] // bs)].astype(np.int32))
+            src_tab_off.append(off)
+            off += src_tabs[-1].size
+
+    # spans: disjoint destination ranges in each destination group's position space
+    n_spans = int(rng.integers(1, 7))
+    dst_pos_space = [0] * c["dst_groups"]
+    raw = []
+    for _ in range(n_spans):
+        g = int(rng.integers(c["src_groups"]))
+        n = int(rng.integers(1, min(120, src_rows[g]) + 1))
+        sp = int(rng.integers(0, src_rows[g] - n + 1))
+        dg = int(rng.integers(c["dst_groups"]))
+        dp = dst_pos_space[dg] + int(rng.integers(0, 40))
+        dst_pos_space[dg] = dp + n
+        delta = int(rng.choice([0, int(rng.integers(-64, 65)), int(rng.integers(-40000, 40001)),
+                                int(rng.integers(-(2**31), 2**31))]))
+        raw.append((sp, dp, n, delta, g, dg))
+
+    dst_blocks = max(-(-p // bs) for p in dst_pos_space) + 3
+    dst_caches = []
+    for _ in range(c["dst_groups"]):
+        dst_caches.append([randn(_paged_shape(dst_blocks, c["dst_layout"], bs, heads, d), dtype,
+                                 gen, sc) for _ in range(layers)])
+    dst_tabs = [rng.permutation(dst_blocks).astype(np.int64) for _ in range(c["dst_groups"])]
+
+    rows, dst_index_parts, d_off = [], [], 0
+    for sp, dp, n, delta, g, dg in raw:
+        s_idx = src_tab_off[g] if c["src_layout"] != "flat" else 0
+        if c["dst_mode"] == "slots":
+            pos = np.arange(dp, dp + n)
+            dst_index_parts.append(dst_tabs[dg][pos // bs] * bs + pos % bs)
+            rows.append((sp, 0, s_idx, d_off, n, delta, g, dg))
+            d_off += n
+        else:
+            rows.append((sp, dp, s_idx, dg * dst_blocks, n, delta, g, dg))
+    if c["dst_mode"] == "slots":
+        dst_index = torch.from_numpy(np.concatenate(dst_index_parts).astype(np.int64))
+    else:
+        dst_index = torch.from_numpy(np.concatenate(dst_tabs).astype(np.int32))
+    src_index = (None if c["src_layout"] == "flat"
+                 else torch.from_numpy(np.concatenate(src_tabs).astype(np.int32)))
+    spans = span_array(rows)
+    k_scale = (torch.from_numpy(rng.uniform(0.01, 0.1, layers).astype(np.float32)) if fp8
+               else None)
+    inv = inv_freq(c["rotary"]) if c["rotary"] else None
+
+    src_cs = CacheSet([[t.to(gpu) for t in row] for row in src_caches], c["src_layout"],
+                      1 if c["src_layout"] == "flat" else bs)
+    dst_cs = CacheSet([[t.to(gpu) for t in row] for row in dst_caches], c["dst_layout"], bs)
+    plan = ShiftPlan(spans, src_cs, dst_cs, inv_freq=inv,
+                     src_mode="flat" if c["src_layout"] == "flat" else "table",
+                     src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
+                     k_scale=k_scale)
+    src_o = oracle_side(src_cs, "flat" if c["src_layout"] == "flat" else "table", src_index)
+    dst_o = oracle_side(dst_cs, c["dst_mode"], dst_index)
+    return plan, dst_cs, spans, src_o, dst_o, inv, k_scale
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_batched_shift_matches_oracle(gpu, seed):
+    c = _case(seed)
+    desc = {k: (str(v) if k == "dtype" else v) for k, v in c.items() if k != "rng"}
+    print(f"case random {desc}", flush=True)
+    plan, dst_cs, spans, src_o, dst_o, inv, k_scale = _build(c, gpu)
+    inv_np = np.zeros(0, np.float32) if inv is None else inv.numpy()
+    orc.shift_spans(oracle_spans(spans), src_o, dst_o, inv_np, dname(c["dtype"]),
+                    None if k_scale is None else k_scale.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for g, row in enumerate(dst_cs.caches):
+        for layer, t in enumerate(row):
+            assert np.array_equal(bits(t), dst_o.caches[g][layer]), f"group {g} layer {layer}"
