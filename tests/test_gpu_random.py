@@ -1,11 +1,14 @@
 """Seeded random batched shifts against the oracle, byte for byte.
 
-Each case draws a geometry (element type, head size, heads, rotary width, layers, block
-size), a source side (flat session stores, or paged NHD / HND caches through block
-tables, one to three groups), a destination side (a paged NHD or HND cache through a
-slot mapping or a block table, one or two groups) and one to six spans with disjoint
-destinations and deltas of both signs, zero and large.  Every destination byte of every
-layer must equal the oracle's, and no error flag may be raised.
+Each case draws:
+* a geometry: element type, head size, heads, rotary width, layers, block size;
+* a source side: flat session stores, or paged NHD / HND caches through block tables,
+  in one to three groups;
+* a destination side: a paged NHD or HND cache through a slot mapping or a block table,
+  or flat session stores, in one or two groups;
+* one to six spans with disjoint destinations and deltas of both signs, zero and large.
+Every destination byte of every layer must equal the oracle's, and no error flag may be
+raised.
 """
 
 from __future__ import annotations
@@ -36,10 +39,10 @@ def _case(seed: int):
     layers = int(rng.integers(1, 4))
     bs = int(rng.choice([16, 16, 32]))
     src_layout = str(rng.choice(["flat", "nhd", "hnd"]))
-    dst_layout = str(rng.choice(["nhd", "hnd"]))
-    dst_mode = str(rng.choice(["slots", "table"]))
+    dst_layout = str(rng.choice(["nhd", "hnd", "flat"]))
+    dst_mode = "flat" if dst_layout == "flat" else str(rng.choice(["slots", "table"]))
     src_groups = int(rng.integers(1, 4))
-    dst_groups = int(rng.integers(1, 3)) if dst_mode == "table" else 1
+    dst_groups = int(rng.integers(1, 3)) if dst_mode != "slots" else 1
     return dict(seed=seed, dtype=dtype, d=d, rotary=rotary, heads=heads, layers=layers,
                 bs=bs, src_layout=src_layout, dst_layout=dst_layout, dst_mode=dst_mode,
                 src_groups=src_groups, dst_groups=dst_groups, rng=rng)
@@ -91,9 +94,12 @@ def _build(c, gpu):
 
     dst_blocks = max(-(-p // bs) for p in dst_pos_space) + 3
     dst_caches = []
-    for _ in range(c["dst_groups"]):
-        dst_caches.append([randn(_paged_shape(dst_blocks, c["dst_layout"], bs, heads, d), dtype,
-                                 gen, sc) for _ in range(layers)])
+    for g in range(c["dst_groups"]):
+        if c["dst_layout"] == "flat":  # a session store: slot = position
+            shape = (dst_pos_space[g] + int(rng.integers(1, 30)), heads, 2 * d)
+        else:
+            shape = _paged_shape(dst_blocks, c["dst_layout"], bs, heads, d)
+        dst_caches.append([randn(shape, dtype, gen, sc) for _ in range(layers)])
     dst_tabs = [rng.permutation(dst_blocks).astype(np.int64) for _ in range(c["dst_groups"])]
 
     rows, dst_index_parts, d_off = [], [], 0
@@ -104,10 +110,14 @@ def _build(c, gpu):
             dst_index_parts.append(dst_tabs[dg][pos // bs] * bs + pos % bs)
             rows.append((sp, 0, s_idx, d_off, n, delta, g, dg))
             d_off += n
+        elif c["dst_mode"] == "flat":
+            rows.append((sp, dp, s_idx, 0, n, delta, g, dg))
         else:
             rows.append((sp, dp, s_idx, dg * dst_blocks, n, delta, g, dg))
     if c["dst_mode"] == "slots":
         dst_index = torch.from_numpy(np.concatenate(dst_index_parts).astype(np.int64))
+    elif c["dst_mode"] == "flat":
+        dst_index = None
     else:
         dst_index = torch.from_numpy(np.concatenate(dst_tabs).astype(np.int32))
     src_index = (None if c["src_layout"] == "flat"
@@ -119,7 +129,8 @@ def _build(c, gpu):
 
     src_cs = CacheSet([[t.to(gpu) for t in row] for row in src_caches], c["src_layout"],
                       1 if c["src_layout"] == "flat" else bs)
-    dst_cs = CacheSet([[t.to(gpu) for t in row] for row in dst_caches], c["dst_layout"], bs)
+    dst_cs = CacheSet([[t.to(gpu) for t in row] for row in dst_caches], c["dst_layout"],
+                      1 if c["dst_layout"] == "flat" else bs)
     plan = ShiftPlan(spans, src_cs, dst_cs, inv_freq=inv,
                      src_mode="flat" if c["src_layout"] == "flat" else "table",
                      src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
@@ -129,7 +140,7 @@ def _build(c, gpu):
     return plan, dst_cs, spans, src_o, dst_o, inv, k_scale
 
 
-@pytest.mark.parametrize("seed", range(32))
+@pytest.mark.parametrize("seed", range(48))
 def test_random_batched_shift_matches_oracle(gpu, seed):
     c = _case(seed)
     desc = {k: (str(v) if k == "dtype" else v) for k, v in c.items() if k != "rng"}
