@@ -156,3 +156,46 @@ def test_random_batched_shift_matches_oracle(gpu, seed):
     for g, row in enumerate(dst_cs.caches):
         for layer, t in enumerate(row):
             assert np.array_equal(bits(t), dst_o.caches[g][layer]), f"group {g} layer {layer}"
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_single_span_matches_oracle(gpu, seed):
+    """The per-layer entry point (``scatter_shifted``, the reference's signature) over
+    random geometries: any element type, head size, rotary width, head count, layout and
+    block size (16, 32 or 24, not a power of two); the source a view into a larger store
+    buffer; distinct random destination slots; deltas of every magnitude."""
+    from marathon_amd import rope_shift, scatter_shifted
+
+    rng = np.random.default_rng(1000 + seed)
+    dtype = DTYPES[seed % len(DTYPES)]
+    d = int(rng.choice([64, 128, 256]))
+    per_chunk = 16 // EB[dtype]
+    rotary = int(rng.choice([r for r in (d // 2, d) if r % (2 * per_chunk) == 0]))
+    heads = int(rng.choice([1, 2, 3, 4, 5, 8, 16]))
+    bs = int(rng.choice([16, 32, 24]))
+    hnd = bool(rng.integers(2))
+    n = int(rng.integers(1, 300))
+    delta = int(rng.choice([0, int(rng.integers(-64, 65)), int(rng.integers(-40000, 40001)),
+                            int(rng.integers(-(2**31), 2**31))]))
+    print(f"case random single span seed={seed} {dtype} d={d} rotary={rotary} heads={heads} "
+          f"bs={bs} hnd={hnd} n={n} delta={delta}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    sc = 0.05
+    start = int(rng.integers(0, 50))
+    buf = randn((start + n + int(rng.integers(0, 20)), heads, 2 * d), dtype, gen, sc)
+    nblocks = -(-n // bs) + int(rng.integers(1, 8))
+    shape = (nblocks, heads, bs, 2 * d) if hnd else (nblocks, bs, heads, 2 * d)
+    kv = randn(shape, dtype, gen, sc)
+    slots = torch.from_numpy(rng.permutation(nblocks * bs)[:n].astype(np.int64))
+    fp8 = dtype == torch.float8_e4m3fn
+    inv = inv_freq(rotary)
+    kv_dev = kv.to(gpu)
+    buf_dev = buf.to(gpu)
+    scatter_shifted(buf_dev[start:start + n], kv_dev, slots.to(gpu), bs, hnd,
+                    rope_shift(delta, d, inv, gpu), **({"k_scale": sc} if fp8 else {}))
+    torch.cuda.synchronize(gpu)
+    want = bits(kv)
+    orc.scatter_shifted(bits(buf[start:start + n]), want, slots.numpy(), bs, hnd, delta,
+                        inv.numpy(), dname(dtype), **({"k_scale": np.float32(sc)} if fp8 else {}))
+    got = bits(kv_dev)
+    assert np.array_equal(got, want), f"{int((got != want).sum())} elements differ"
