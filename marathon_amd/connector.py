@@ -360,7 +360,6 @@ class ShiftLoader:
             )
         return tokens * len(names)
 
-
     def _source_rows(self, load: Load, name: str) -> torch.Tensor:
         """``[n, heads, 2D]`` rows the load read, without the store's read accounting."""
         n = load.n
