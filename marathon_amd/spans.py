@@ -32,11 +32,17 @@ MODES = {"flat": _lib.MKV_ADDR_FLAT, "slots": _lib.MKV_ADDR_SLOTS, "table": _lib
 @dataclass
 class CacheSet:
     """``caches[group][layer]`` of one layout; every tensor has the same trailing shape,
-    strides and dtype (groups may differ in their number of blocks / rows)."""
+    strides and dtype (groups may differ in their number of blocks / rows).
+
+    Rows are fused, ``[..., 2D]`` with K then V, unless ``v_caches`` is given: then
+    ``caches`` hold K and ``v_caches`` V, as separate tensors of the same shape and
+    strides with rows ``[..., D]`` (split K and V planes, e.g. ``kv[0]`` and ``kv[1]``
+    of a ``[2, blocks, bs, heads, D]`` cache)."""
 
     caches: list
     layout: str  # "flat" | "hnd" | "nhd"
     block_size: int = 1
+    v_caches: list | None = None
 
     def __post_init__(self):
         if self.layout not in ("flat", "hnd", "nhd"):
@@ -45,6 +51,18 @@ class CacheSet:
             raise ValueError("empty CacheSet")
         if isinstance(self.caches[0], torch.Tensor):
             self.caches = [list(self.caches)]
+        if self.v_caches is not None:
+            if isinstance(self.v_caches[0], torch.Tensor):
+                self.v_caches = [list(self.v_caches)]
+            if len(self.v_caches) != len(self.caches) or any(
+                    len(kr) != len(vr) for kr, vr in zip(self.caches, self.v_caches)):
+                raise ValueError("v_caches must match caches group by group, layer by layer")
+            for kr, vr in zip(self.caches, self.v_caches):
+                for k, v in zip(kr, vr):
+                    if (k.shape != v.shape or k.stride() != v.stride() or k.dtype != v.dtype
+                            or k.device != v.device):
+                        raise ValueError("a V tensor differs from its K tensor in shape, "
+                                         "strides, dtype or device")
         first = self.caches[0][0]
         want_dim = 3 if self.layout == "flat" else 4
         for row in self.caches:
@@ -83,8 +101,12 @@ class CacheSet:
         return self.first.shape[1] if self.layout in ("flat", "hnd") else self.first.shape[2]
 
     @property
+    def split(self) -> bool:
+        return self.v_caches is not None
+
+    @property
     def head_size(self) -> int:
-        return self.first.shape[-1] // 2
+        return self.first.shape[-1] if self.split else self.first.shape[-1] // 2
 
     @property
     def strides(self) -> tuple[int, int, int]:
@@ -104,7 +126,11 @@ class CacheSet:
         if got is None:
             eb = self.first.element_size()
             k = np.array([[t.data_ptr() for t in row] for row in self.caches], dtype=np.uint64)
-            v = k + np.uint64(self.head_size * eb)
+            if self.split:
+                v = np.array([[t.data_ptr() for t in row] for row in self.v_caches],
+                             dtype=np.uint64)
+            else:
+                v = k + np.uint64(self.head_size * eb)
             caps = np.array([self.slots_of(row[0]) for row in self.caches], dtype=np.int64)
             got = self._bases = (k, v, caps, int(caps.min()), bool(np.all(caps == caps[0])))
         return got

@@ -164,3 +164,27 @@ def test_rope_shift_asserts_rotary_fits():
     inv = torch.ones(80)
     with pytest.raises(AssertionError, match="rotary 160 > head_size 128"):
         rope_shift(1, 128, inv, "cpu")
+
+
+def test_cacheset_split_planes_are_validated_and_sized():
+    """Split K and V planes: rows of D (not 2D), V base addresses from the V tensors,
+    and a V tensor that differs from its K tensor is refused."""
+    import numpy as np
+
+    from marathon_amd.spans import CacheSet
+
+    k = [torch.zeros(10, 16, 4, 128, dtype=torch.bfloat16) for _ in range(3)]
+    v = [torch.zeros(10, 16, 4, 128, dtype=torch.bfloat16) for _ in range(3)]
+    cs = CacheSet([k], "nhd", 16, v_caches=[v])
+    assert (cs.split, cs.heads, cs.head_size, cs.layers) == (True, 4, 128, 3)
+    kb, vb, caps, min_cap, uniform = cs.base_tables()
+    assert list(kb[0]) == [t.data_ptr() for t in k]
+    assert list(vb[0]) == [t.data_ptr() for t in v]
+    assert min_cap == 160 and uniform and caps.dtype == np.int64
+    fused = CacheSet([[torch.zeros(10, 16, 4, 256, dtype=torch.bfloat16)]], "nhd", 16)
+    assert (fused.split, fused.head_size) == (False, 128)
+    with pytest.raises(ValueError, match="differs from its K tensor"):
+        CacheSet([k], "nhd", 16, v_caches=[[*v[:2], torch.zeros(10, 16, 4, 64,
+                                                                dtype=torch.bfloat16)]])
+    with pytest.raises(ValueError, match="group by group"):
+        CacheSet([k], "nhd", 16, v_caches=[v[:2]])

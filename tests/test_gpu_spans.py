@@ -213,6 +213,71 @@ def test_batched_multi_token_passes_match_oracle(gpu, dtype, heads, d, rotary):
         assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
 
 
+@pytest.mark.parametrize("plane_axis", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_split_k_and_v_planes_match_oracle(gpu, dtype, plane_axis):
+    """K and V in separate tensors: a fused flat store (two sessions) into the split
+    planes of one cache, ``[2, blocks, bs, heads, D]`` (plane_axis 0) or ``[blocks, 2,
+    bs, heads, D]`` (plane_axis 1, strided views), then those planes back into split
+    flat stores.  Against the oracle on the same rows fused."""
+    from marathon_amd.spans import CacheSet, ShiftPlan
+    from tests.helpers import randn
+
+    print(f"case split K/V planes {dtype} axis={plane_axis}", flush=True)
+    g = torch.Generator().manual_seed(31 + plane_axis)
+    layers, heads, d, bs, nblk = 2, 4, 128, 16, 40
+    sc = 0.05
+    bufs = [[randn((n, heads, 2 * d), dtype, g, sc) for _ in range(layers)] for n in (300, 200)]
+    shape = (2, nblk, bs, heads, d) if plane_axis == 0 else (nblk, 2, bs, heads, d)
+    kvs = [randn(shape, dtype, g, sc) for _ in range(layers)]
+
+    def planes(t):
+        return (t[0], t[1]) if plane_axis == 0 else (t[:, 0], t[:, 1])
+
+    table = torch.randperm(nblk, generator=torch.Generator().manual_seed(7)).tolist()
+    spans = [(5, 3, 0, 0, 121, -41, 0, 0), (150, 130, 0, 0, 138, 1999, 0, 0),
+             (0, 300, 0, 0, 191, 0, 1, 0), (17, 520, 0, 0, 79, -7, 1, 0)]
+    k_scale = torch.tensor([0.031, 0.066]) if dtype == torch.float8_e4m3fn else None
+    kvs_dev = [t.to(gpu) for t in kvs]
+    dst = CacheSet([[planes(t)[0] for t in kvs_dev]], "nhd", bs,
+                   v_caches=[[planes(t)[1] for t in kvs_dev]])
+    src = CacheSet([[b.to(gpu) for b in row] for row in bufs], "flat")
+    tab = torch.tensor(table, dtype=torch.int32)
+    plan = ShiftPlan(span_array(spans), src, dst, inv_freq=inv_freq(128), src_mode="flat",
+                     dst_mode="table", dst_index=tab, k_scale=k_scale)
+    # the oracle works on fused rows: the same planes, concatenated
+    fused = [torch.cat(planes(t), dim=-1) for t in kvs]
+    src_o = oracle_side(src, "flat", None)
+    dst_o = orc.Side([[bits(t) for t in fused]], "nhd", bs, "table", tab.numpy())
+    orc.shift_spans(oracle_spans(span_array(spans)), src_o, dst_o, inv_freq(128).numpy(),
+                    dname(dtype), None if k_scale is None else k_scale.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer, t in enumerate(kvs_dev):
+        k, v = planes(t)
+        want = dst_o.caches[0][layer]
+        assert np.array_equal(bits(k), want[..., :d]), f"K layer {layer}"
+        assert np.array_equal(bits(v), want[..., d:]), f"V layer {layer}"
+
+    # and back: the planes (paged, split) into split flat stores, delta 0
+    back_k = [torch.zeros(700, heads, d, dtype=dtype, device=gpu) for _ in range(layers)]
+    back_v = [torch.zeros(700, heads, d, dtype=dtype, device=gpu) for _ in range(layers)]
+    save = ShiftPlan(span_array([(0, 0, 0, 0, 600, 0, 0, 0)]), dst, CacheSet(
+        [back_k], "flat", v_caches=[back_v]), inv_freq=None, src_mode="table", src_index=tab,
+        dst_mode="flat")
+    save.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    pos = torch.arange(600)
+    slot = tab.long()[pos // bs] * bs + pos % bs
+    for layer, t in enumerate(kvs_dev):
+        k, v = planes(t)
+        assert torch.equal(back_k[layer][:600], k[slot // bs, slot % bs])
+        assert torch.equal(back_v[layer][:600], v[slot // bs, slot % bs])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
 def test_batched_extreme_deltas_match_oracle(gpu, dtype):
     """The plan kernel evaluates each span's cos/sin on the device: int32 extremes and
