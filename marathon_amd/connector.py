@@ -151,12 +151,16 @@ class _CacheSets:
         self.block_size = block_size
         self._sets: dict[str, tuple] = {}
 
-    def get(self, role: str, caches: list, layout: str, block_size: int | None = None) -> CacheSet:
-        key = tuple(tuple(id(t) for t in row) for row in caches)
+    def get(self, role: str, caches: list, layout: str, block_size: int | None = None,
+            v_caches: list | None = None) -> CacheSet:
+        key = (tuple(tuple(id(t) for t in row) for row in caches),
+               None if v_caches is None else tuple(tuple(id(t) for t in row) for row in v_caches))
         hit = self._sets.get(role)
         if hit is None or hit[0] != key:
             bs = self.block_size if block_size is None else block_size
-            hit = self._sets[role] = (key, CacheSet([list(r) for r in caches], layout, bs))
+            hit = self._sets[role] = (key, CacheSet(
+                [list(r) for r in caches], layout, bs,
+                v_caches=None if v_caches is None else [list(r) for r in v_caches]))
         return hit[1]
 
 
@@ -208,6 +212,25 @@ def detect_hnd(shape, block_size: int) -> bool:
     return hnd
 
 
+def paged_planes(kv: torch.Tensor, block_size: int):
+    """``(layout, k, v)`` of one layer's paged cache.
+
+    4-D: the reference's fused cache (:396-402), rows ``[2D]``; ``k`` is the cache and
+    ``v`` is None.  5-D: split K and V planes along the axis of size 2, as vLLM's
+    ``[2, blocks, bs, heads, D]`` and ``[blocks, 2, bs, heads, D]`` caches hold them;
+    ``k`` and ``v`` are the two planes (views), rows ``[D]``.  The layout of the 4-D
+    cache or plane follows :func:`detect_hnd`.
+    """
+    shape = tuple(kv.shape)
+    if len(shape) == 4:
+        return ("hnd" if detect_hnd(shape, block_size) else "nhd"), kv, None
+    if len(shape) != 5 or 2 not in shape[:2]:
+        raise ValueError(f"expected a fused 4-D or a split 5-D KV cache, got {shape}")
+    axis = 0 if shape[0] == 2 else 1
+    k, v = kv.select(axis, 0), kv.select(axis, 1)
+    return ("hnd" if detect_hnd(tuple(k.shape), block_size) else "nhd"), k, v
+
+
 def accept_multi(loads: list, num_computed: int, num_prompt_tokens: int, block_size: int,
                  covers) -> list:
     """Block-align every segment of a multi-segment load (vllm_shift_connector.py:225-245).
@@ -253,17 +276,26 @@ class ShiftLoader:
         self.k_scales = k_scales or {}
         self.timing = timing
         self._kv: dict[str, torch.Tensor] = {}
+        self._planes: dict[str, tuple] = {}  # name -> (K, V or None), see paged_planes
+        self.layout: str | None = None
         self.hnd: bool | None = None
+        self.split = False
         self.head_size: int | None = None
         self.last_plan: ShiftPlan | None = None
         self._sets = _CacheSets(self.block_size)
 
     def register_kv_caches(self, kv_caches: dict) -> None:
-        """Record the per-layer paged caches and their layout (:393-412)."""
+        """Record the per-layer paged caches and their layout (:393-412): fused 4-D, as
+        the reference takes them, or split K and V planes (5-D, :func:`paged_planes`)."""
         self._kv = dict(kv_caches)
-        shape = next(iter(self._kv.values())).shape
-        self.hnd = detect_hnd(shape, self.block_size)
-        self.head_size = shape[3] // 2
+        self._planes = {}
+        for name, t in self._kv.items():
+            layout, k, v = paged_planes(t, self.block_size)
+            self._planes[name] = (k, v)
+        self.layout = layout
+        self.hnd = layout == "hnd"
+        self.split = v is not None
+        self.head_size = k.shape[3] if self.split else k.shape[3] // 2
         one = next(iter(self._kv.values()))
         if one.is_cuda:
             _lib.lib()  # the kernels are compiled ahead of time: only load the library
@@ -321,7 +353,9 @@ class ShiftLoader:
             for load, (dpos, didx) in zip(taken, dst_rows):
                 rows.append((load.src_start, dpos, 0, didx, load.n, int(load.delta),
                              groups[load.session], 0))
-        dst = self._sets.get("paged", [list(self._kv.values())], "hnd" if self.hnd else "nhd")
+        planes = list(self._planes.values())
+        dst = self._sets.get("paged", [[k for k, _ in planes]], self.layout,
+                             v_caches=[[v for _, v in planes]] if self.split else None)
         k_scale = None
         if dst.first.dtype == torch.float8_e4m3fn:
             k_scale = torch.tensor([float(self.k_scales.get(name, 1.0)) for name in names])
@@ -377,15 +411,19 @@ class ShiftLoader:
         dimensions past ``rotary`` and V as stored.  fp8 rows are compared dequantised
         with the layer's K scale (V raw).  The figures are logged and kept in
         :attr:`verify_log`."""
-        kv = self._kv[name]
+        kp, vp = self._planes[name]
         row = self._source_rows(load, name)
         d = row.shape[-1] // 2
         rot = 2 * int(self.inv_freq.numel())
         slots = (load.slots if load.slots is not None else
                  host_slots(load.block_ids, load.paged_pos, load.paged_pos + load.n,
-                            self.block_size)).to(kv.device, torch.int64)
+                            self.block_size)).to(kp.device, torch.int64)
         blk, off = slots // self.block_size, slots % self.block_size
-        got = kv[blk, :, off] if self.hnd else kv[blk, off]
+
+        def rows_of(t):
+            return t[blk, :, off] if self.hnd else t[blk, off]
+
+        got = rows_of(kp) if vp is None else torch.cat((rows_of(kp), rows_of(vp)), dim=-1)
         scale = 1.0 if k_scale is None else float(k_scale[layer])
         k = row[..., :d].to(torch.float32) * scale
         want_k = torch.cat((_rerotate(k[..., :rot], int(load.delta), self.inv_freq),
@@ -574,11 +612,24 @@ class ShiftSaver:
         self.last_plan: ShiftPlan | None = None
         self._sets = _CacheSets(self.block_size)
         self._pending: list = []  # deferred: (layer name, paged cache, the step's saves)
+        self._plane_memo: dict[int, tuple] = {}  # id(cache) -> (cache, layout, K, V)
+
+    def _planes(self, t: torch.Tensor):
+        hit = self._plane_memo.get(id(t))
+        if hit is None or hit[0] is not t:
+            if len(self._plane_memo) > 4096:  # caches replaced many times over
+                self._plane_memo.clear()
+            hit = self._plane_memo[id(t)] = (t, *paged_planes(t, self.block_size))
+        return hit[1:]
 
     def _plan(self, names: list, caches: list, saves: list) -> int:
-        first = caches[0]
-        hnd = detect_hnd(first.shape, self.block_size)
-        row_shape = (first.shape[1] if hnd else first.shape[2], first.shape[3])
+        planes = [self._planes(t) for t in caches]
+        layout, first, v_first = planes[0]
+        hnd = layout == "hnd"
+        split = v_first is not None
+        # the store holds fused rows [heads, 2D] whichever way the paged cache keeps them
+        row_shape = (first.shape[1] if hnd else first.shape[2],
+                     first.shape[3] * (2 if split else 1))
         blocky = isinstance(self.store, BlockShiftStore)
         groups: dict[str, int] = {}
         bufs: list[list] = []
@@ -627,7 +678,8 @@ class ShiftSaver:
                 rows.append((spos, int(sv.dst_start), sidx, 0, sv.n, 0, 0, groups[sv.session]))
         plan = ShiftPlan(
             np.array(rows, dtype=_lib.SPAN_DTYPE),
-            self._sets.get("paged", [caches], "hnd" if hnd else "nhd"),
+            self._sets.get("paged", [[k for _, k, _ in planes]], layout,
+                           v_caches=[[v for _, _, v in planes]] if split else None),
             dst,
             inv_freq=None,
             src_mode=src_mode,

@@ -382,3 +382,56 @@ def test_deferred_per_layer_saves_equal_one_save_all(gpu):
     assert stores[0].stats() == stores[1].stats()
     for name in kv:
         assert torch.equal(stores[0].read("s", name, 0, 500), stores[1].read("s", name, 0, 500))
+
+
+@pytest.mark.parametrize("plane_axis", [0, 1])
+@pytest.mark.parametrize("store", ["flat", "blocks"])
+def test_split_planes_through_the_connector(gpu, store, plane_axis):
+    """vLLM caches that keep K and V in separate planes ([2, blocks, bs, heads, D] or
+    [blocks, 2, bs, heads, D]) save and load exactly as the fused 4-D cache holding the
+    same rows: the same store bytes, the same loaded rows, and the read-back check."""
+    print(f"case split planes store={store} axis={plane_axis}", flush=True)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(17 + plane_axis)
+    nblk, layers = 64, 3
+    names = [f"l{i}" for i in range(layers)]
+    ks = [torch.randn(nblk, BS, H, D, device=gpu, generator=g).to(torch.bfloat16)
+          for _ in names]
+    vs = [torch.randn(nblk, BS, H, D, device=gpu, generator=g).to(torch.bfloat16)
+          for _ in names]
+    fused = {n: torch.cat((k, v), dim=-1) for n, k, v in zip(names, ks, vs)}
+    split = {n: torch.stack((k, v), dim=plane_axis) for n, k, v in zip(names, ks, vs)}
+
+    def make_store():
+        if store == "flat":
+            return ShiftStore(budget_tokens=4096, device=str(gpu), slab=512)
+        return BlockShiftStore(budget_tokens=4096, device=str(gpu), block_size=BS)
+
+    st_f, st_s = make_store(), make_store()
+    table = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).tolist()
+    saves = [Save.from_blocks("s", table, 0, 500)]
+    assert ShiftSaver(st_f, BS).save_all(fused, saves) == 500 * layers
+    assert ShiftSaver(st_s, BS).save_all(split, saves) == 500 * layers
+    torch.cuda.synchronize(gpu)
+    for n in names:
+        assert torch.equal(st_f.read("s", n, 0, 500), st_s.read("s", n, 0, 500)), n
+
+    inv = inv_freq_for(D, 1e6)
+    out_f = {n: torch.zeros_like(t) for n, t in fused.items()}
+    out_s = {n: torch.zeros_like(t) for n, t in split.items()}
+    lf, ls = ShiftLoader(st_f, BS, inv), ShiftLoader(st_s, BS, inv, verify=True)
+    lf.register_kv_caches(out_f)
+    ls.register_kv_caches(out_s)
+    assert ls.split and ls.layout == "nhd" and not lf.split
+    dst = torch.randperm(nblk, generator=torch.Generator().manual_seed(4)).tolist()
+    loads = [Load.from_blocks("s", dst, 37, 37 + 250, 37),
+             Load.from_blocks("s", dst, 300, 300 + 150, -13)]
+    assert lf.start_load_kv(loads) == ls.start_load_kv(loads) == 400 * layers
+    torch.cuda.synchronize(gpu)
+    for n in names:
+        k_out, v_out = (out_s[n][0], out_s[n][1]) if plane_axis == 0 else (
+            out_s[n][:, 0], out_s[n][:, 1])
+        assert torch.equal(k_out, out_f[n][..., :D]), n
+        assert torch.equal(v_out, out_f[n][..., D:]), n
+    assert len(ls.verify_log) == 2 * layers
+    assert all(e["v_exact"] and e["max_rel"] < 4e-3 for e in ls.verify_log)

@@ -11,7 +11,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from marathon_amd.connector import accept_multi, detect_hnd
+from marathon_amd.connector import accept_multi, detect_hnd, paged_planes
 from marathon_amd.shift_store import (
     LoadDecision,
     SessionTable,
@@ -288,3 +288,21 @@ def test_store_from_config_follows_the_reference_order(monkeypatch):
     assert (st.budget, st.device, st.allocate, st.session_cap) == (7000, "cpu", True, 3000)
     bst = store_from_config({"store_tokens": 640}, worker=True, block_layout=True)
     assert isinstance(bst, BlockShiftStore) and bst.budget == 640 and bst.pool_blocks == 40
+
+
+def test_paged_planes_split_and_fused_layouts():
+    """Fused 4-D caches pass through; 5-D caches split along their axis of size 2 into K
+    and V planes (vLLM's [2, blocks, bs, heads, D] and [blocks, 2, bs, heads, D])."""
+    fused = torch.zeros(6, 8, 16, 256)
+    assert paged_planes(fused, 16) == ("hnd", fused, None)
+    a0 = torch.arange(2 * 6 * 16 * 4 * 128, dtype=torch.float32).reshape(2, 6, 16, 4, 128)
+    layout, k, v = paged_planes(a0, 16)
+    assert layout == "nhd" and torch.equal(k, a0[0]) and torch.equal(v, a0[1])
+    a1 = a0.permute(1, 0, 2, 3, 4)  # [blocks, 2, bs, heads, D], strided planes
+    layout, k, v = paged_planes(a1, 16)
+    assert layout == "nhd" and torch.equal(k, a0[0]) and torch.equal(v, a0[1])
+    assert k.data_ptr() == a0[0].data_ptr() and v.data_ptr() == a0[1].data_ptr()
+    hnd = torch.zeros(2, 6, 4, 16, 128)
+    assert paged_planes(hnd, 16)[0] == "hnd"
+    with pytest.raises(ValueError, match="fused 4-D or a split 5-D"):
+        paged_planes(torch.zeros(3, 6, 16, 4, 128), 16)
