@@ -24,6 +24,8 @@ Prints one JSON line.  Also measured, in the same line:
   rows of its published table.
 * ``tp_shares``: the headline shift at 4, 2 and 1 KV heads (one GPU's share at TP 2, 4,
   8), bf16 and fp8.
+* ``dst_layouts``: the headline shift into fused NHD caches and into caches that keep K
+  and V in separate planes, beside the fused HND headline.
 """
 
 from __future__ import annotations
@@ -361,6 +363,51 @@ def tp_shares(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def dst_layouts(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: the headline shift into each paged-cache layout the connector
+    takes -- fused HND (the headline), fused NHD, and K/V split into planes as
+    ``[2, blocks, 16, heads, D]`` and ``[blocks, 2, 16, heads, D]``."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+    from marathon_amd.spans import CacheSet, ShiftPlan
+
+    wl = W.qwen3_14b_multispan(dev)
+    nblk, layers = wl.dst.first.shape[0], wl.layers
+    heads, d = wl.dst.heads, wl.dst.head_size
+    dst_hnd = wl.dst
+    wl.dst = None
+
+    def run(dst):
+        plan = ShiftPlan(wl.spans, wl.src, dst, inv_freq=wl.inv_freq, src_mode=wl.src_mode,
+                         src_index=wl.src_index, dst_mode=wl.dst_mode, dst_index=wl.dst_index)
+        warm_up(lambda: plan.launch(stream.cuda_stream))
+        _, per = time_plan(plan, max(steps, 50), warmup, stream)
+        ms = float(np.median(per))
+        gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+        return {"ms": round(ms, 4), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+
+    out = {"fused_hnd": run(dst_hnd)}
+    del dst_hnd
+    torch.cuda.empty_cache()
+    nhd = [torch.zeros(nblk, 16, heads, 2 * d, dtype=torch.bfloat16, device=dev)
+           for _ in range(layers)]
+    out["fused_nhd"] = run(CacheSet([nhd], "nhd", 16))
+    del nhd
+    torch.cuda.empty_cache()
+    for axis, name in ((0, "split_2_blocks_bs_heads_d"), (1, "split_blocks_2_bs_heads_d")):
+        shape = (2, nblk, 16, heads, d) if axis == 0 else (nblk, 2, 16, heads, d)
+        caches = [torch.zeros(shape, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+        out[name] = run(CacheSet([[c.select(axis, 0) for c in caches]], "nhd", 16,
+                                 v_caches=[[c.select(axis, 1) for c in caches]]))
+        del caches
+        torch.cuda.empty_cache()
+    del wl
+    torch.cuda.empty_cache()
+    return out
+
+
 def connector_step(dev, steps: int, warmup: int) -> dict:
     """Worker load steps through the connector: a session held in the block-layout store,
     loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
@@ -527,6 +574,8 @@ def main() -> int:
                     "multi-span and batched-session workloads")
     ap.add_argument("--no-tp-shares", action="store_true",
                     help="skip the timings of one GPU's share at 4, 2 and 1 KV heads")
+    ap.add_argument("--no-dst-layouts", action="store_true",
+                    help="skip the headline shift into the other paged-cache layouts")
     ap.add_argument("--no-connector-step", action="store_true",
                     help="skip the end-to-end connector load and save step timings")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -595,6 +644,9 @@ def main() -> int:
     if not args.no_tp_shares:
         log("tensor-parallel shares of the headline shift (4, 2, 1 KV heads)")
         extra["tp_shares"] = tp_shares(dev, side_steps, args.warmup, stream)
+    if not args.no_dst_layouts:
+        log("destination layouts (fused HND / NHD, split K/V planes)")
+        extra["dst_layouts"] = dst_layouts(dev, side_steps, args.warmup, stream)
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
         extra["connector_step"] = connector_step(dev, side_steps, args.warmup)
