@@ -19,7 +19,10 @@
 //     instruction moves whole, contiguous runs (full 128-byte lines).
 //   * When heads is a multiple of the rows a wave covers, every row of a wave pass
 //     belongs to one token: the token's metadata is read with scalar loads and the
-//     lane address is (uniform base) + (per-lane 32-bit constant).
+//     lane address is (uniform base) + (per-lane 32-bit constant).  Otherwise (fewer
+//     heads, e.g. one GPU's share under tensor parallelism) each lane reads its own
+//     token's record, and the wave's shared base-address row comes through scalar
+//     loads.
 //   * rotate_half needs chunk j +- rotary/2: it comes from the partner lane through
 //     ds_bpermute (no second global read of K).
 //   * Batched shifts first run a small plan kernel that resolves every token's source
