@@ -241,3 +241,68 @@ def test_host_slots_match_the_reference_lists():
     assert torch.equal(ld.slots, slots(blocks, 16, 96, BS)) and ld.src_start == 9
     assert sv.dst_start == 0 and torch.equal(sv.slots, slots(blocks, 0, 120, BS))
     assert s._params["r"]["save"] is True  # the one-shot downgrade
+
+
+def _random_edit_sessions(w: FingerprintWorker, seed: int, turns: int, sessions: int):
+    """Sessions taking turns; each turn may rewrite any earlier message (shorter or
+    longer), and the reused span is what the previous prompt held after it."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    state = {f"s{k}": ([], None) for k in range(sessions)}
+    edits = 0
+    for t in range(turns):
+        name = f"s{int(rng.integers(sessions))}"
+        messages, prev = state[name]
+        load = None
+        if prev is not None and messages and rng.random() < 0.7:
+            i = int(rng.integers(len(messages)))
+            messages[i] = {"role": messages[i]["role"],
+                           "content": f"edit {t} " + "x" * int(rng.integers(0, 120))}
+            new = _prompt(messages)[1]
+            old_start = sum(len(p) for p in prev[: i + 1])
+            new_start = sum(len(p) for p in new[: i + 1])
+            end = new_start + sum(len(p) for p in prev[i + 1:])
+            if end > new_start:
+                load = {"dst_start": new_start, "dst_end": end, "delta": new_start - old_start}
+        messages.append({"role": "user", "content": f"{name} turn {t}. " + FILLER *
+                         int(rng.integers(1, 4))})
+        ids, pieces = _prompt(messages)
+        lo = -(-load["dst_start"] // BS) * BS if load else 0
+        hi = load["dst_end"] // BS * BS if load else 0
+        n_out = int(rng.integers(0, 6))
+        if load and hi - lo >= BS and 0 < lo and hi < len(ids):
+            edits += 1
+            w.generate(ids[:lo], name, 1)
+            w.generate(ids, name, n_out, load={**load, "dst_start": lo, "dst_end": hi},
+                       save="full")
+        else:
+            w.generate(ids, name, n_out, save="full")
+        messages.append({"role": "assistant", "content": f"ok {t} " + "y" * int(rng.integers(0, 40))})
+        state[name] = (messages, pieces)
+    return edits
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("store,budget", [("flat", 1 << 20), ("blocks", 1 << 16),
+                                          ("flat", 6000), ("blocks", 6000)])
+def test_random_edit_sessions_keep_every_coordinate(seed, store, budget):
+    """Edits anywhere in the history, of any length, in three interleaved sessions, with
+    stores large enough for all of them or small enough to evict: every position of
+    every prompt still holds its own token.  A load the store can no longer serve is
+    declined (and recomputed), never guessed at; with room for every session, edit
+    turns reuse."""
+    w = FingerprintWorker(seed % 2 == 1, store)
+    if budget != (1 << 20 if store == "flat" else 1 << 16):
+        if store == "flat":
+            w.store = ShiftStore(budget, device="cpu")
+            w.sched.store = ShiftStore(budget, allocate=False)
+        else:
+            w.store = BlockShiftStore(budget, device="cpu", block_size=BS)
+            w.sched.store = BlockShiftStore(budget, allocate=False, block_size=BS)
+    edits = _random_edit_sessions(w, seed, 24, 3)
+    assert w.corruptions == [], w.corruptions[:3]
+    assert all("store no longer holds" in why or "local hit" in why for why in w.sched.declines), \
+        w.sched.declines[:3]
+    if budget >= 1 << 16:  # room for every session: every edit turn reuses
+        assert len(w.loads) == edits > 0, (len(w.loads), edits, w.sched.declines[:3])
