@@ -47,6 +47,7 @@ class RealKVEngine:
         self.loader.register_kv_caches(self.kv)
         self.saver = ShiftSaver(self.store, BS)
         self.next_block = 0
+        self.n_blocks = blocks
         self.prefix: dict[tuple, int] = {}
         self.shifts = torch.zeros(blocks * BS, dtype=torch.int32)  # per slot: re-rotations
         self.store_shifts: dict[str, torch.Tensor] = {}
@@ -64,6 +65,9 @@ class RealKVEngine:
     def _write_fresh(self, blocks, ids, lo, hi):
         if hi <= lo:
             return
+        # host-side bound: the paged cache holds n_blocks blocks (torch indexing on the
+        # device must never go out of range)
+        assert self.next_block <= self.n_blocks, "the test ran out of paged blocks"
         sl = slots(blocks, lo, hi, BS)
         k, v = self.fresh(torch.tensor(ids[lo:hi]), torch.arange(lo, hi))
         row = torch.cat((k.to(torch.bfloat16), v), -1)
@@ -435,3 +439,17 @@ def test_split_planes_through_the_connector(gpu, store, plane_axis):
         assert torch.equal(v_out, out_f[n][..., D:]), n
     assert len(ls.verify_log) == 2 * layers
     assert all(e["v_exact"] and e["max_rel"] < 4e-3 for e in ls.verify_log)
+
+
+@pytest.mark.parametrize("store,device_slots", [("flat", False), ("blocks", True)])
+def test_random_edit_sessions_through_the_real_kernels(gpu, store, device_slots):
+    """Edits anywhere in the history, in three interleaved sessions, every decision
+    through the scheduler half, every load and save through the HIP kernels: after every
+    request every position of every layer holds its token's KV (V bit-exact, K within
+    its shifts' rounding)."""
+    from tests.test_scheduler import _random_edit_sessions
+
+    print(f"case random edit sessions store={store} device_slots={device_slots}", flush=True)
+    eng = ScheduledKVEngine(gpu, store=store, device_slots=device_slots)
+    edits = _random_edit_sessions(eng, 5, 14, 3)
+    assert eng.loads == edits > 0, (eng.loads, edits, eng.declines)
