@@ -24,6 +24,8 @@ Prints one JSON line.  Also measured, in the same line:
   rows of its published table.
 * ``tp_shares``: the headline shift at 4, 2 and 1 KV heads (one GPU's share at TP 2, 4,
   8), bf16 and fp8.
+* ``ceilings``: a plain elementwise copy of the same bytes, and the headline with its
+  block tables made the identity: what the GPU streams with nothing scattered.
 * ``dst_layouts``: the headline shift into fused NHD caches and into caches that keep K
   and V in separate planes, beside the fused HND headline.
 """
@@ -363,6 +365,59 @@ def tp_shares(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def ceilings(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: what this GPU streams with nothing scattered, beside the headline.
+
+    * ``elementwise_copy``: torch's elementwise kernel (``neg``) over 3.6 GB of bf16,
+      reading it once and writing it once (the headline moves 7.26 GB the same way).
+    * ``headline_identity_tables``: the headline shift through the same kernel, with the
+      source block table and the destination slots made the identity, so every span is
+      one contiguous run on each side.  The gap between this and the headline is what
+      scattered 64 KB blocks cost.
+    """
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+
+    out = {}
+    n = 22141 * 40 * 8 * 256  # the headline's K and V elements (tokens x layers x heads x 2D)
+    a = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(a)
+    warm_up(lambda: torch.neg(a, out=b))
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record(stream)
+        torch.neg(a, out=b)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    ms = float(np.median([s_.elapsed_time(e) for s_, e in zip(starts, ends)]))
+    moved = 2 * a.numel() * a.element_size()
+    out["elementwise_copy"] = {"bytes": moved, "ms": round(ms, 4),
+                               "GB_s": round(moved / (ms / 1e3) / 1e9, 1),
+                               "frac_of_peak": round(moved / (ms / 1e3) / 1e9 / PEAK_GBS, 4)}
+    del a, b
+    torch.cuda.empty_cache()
+
+    wl = W.qwen3_14b_multispan(dev)
+    wl.src_index = torch.arange(wl.src.first.shape[0], dtype=torch.int32)
+    wl.dst_index = torch.cat([torch.arange(int(r["dst_pos"]), int(r["dst_pos"]) + int(r["n_tokens"]),
+                                           dtype=torch.int64) for r in wl.spans])
+    if int(wl.dst_index.max()) >= wl.dst.first.shape[0] * 16:
+        raise AssertionError("identity slots exceed the destination cache")
+    plan = wl.plan()
+    warm_up(lambda: plan.launch(stream.cuda_stream))
+    _, per = time_plan(plan, max(steps, 50), warmup, stream)
+    ms = float(np.median(per))
+    gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+    out["headline_identity_tables"] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
+                                       "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    del wl, plan
+    torch.cuda.empty_cache()
+    return out
+
+
 def dst_layouts(dev, steps: int, warmup: int, stream) -> dict:
     """Informational: the headline shift into each paged-cache layout the connector
     takes -- fused HND (the headline), fused NHD, and K/V split into planes as
@@ -574,6 +629,8 @@ def main() -> int:
                     "multi-span and batched-session workloads")
     ap.add_argument("--no-tp-shares", action="store_true",
                     help="skip the timings of one GPU's share at 4, 2 and 1 KV heads")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the plain elementwise copy and the identity-table headline")
     ap.add_argument("--no-dst-layouts", action="store_true",
                     help="skip the headline shift into the other paged-cache layouts")
     ap.add_argument("--no-connector-step", action="store_true",
@@ -644,6 +701,9 @@ def main() -> int:
     if not args.no_tp_shares:
         log("tensor-parallel shares of the headline shift (4, 2, 1 KV heads)")
         extra["tp_shares"] = tp_shares(dev, side_steps, args.warmup, stream)
+    if not args.no_ceilings:
+        log("ceilings: elementwise copy, the headline with identity tables")
+        extra["ceilings"] = ceilings(dev, side_steps, args.warmup, stream)
     if not args.no_dst_layouts:
         log("destination layouts (fused HND / NHD, split K/V planes)")
         extra["dst_layouts"] = dst_layouts(dev, side_steps, args.warmup, stream)
