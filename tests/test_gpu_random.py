@@ -23,6 +23,9 @@ from tests.helpers import bits, dname, inv_freq, oracle_side, oracle_spans, rand
 
 pytestmark = pytest.mark.gpu
 
+# more seeds for a longer sweep: MKV_RANDOM_CASES=2000 python -m pytest tests/test_gpu_random.py
+_EXTRA = int(__import__("os").environ.get("MKV_RANDOM_CASES", "0"))
+
 DTYPES = [torch.bfloat16, torch.float16, torch.float32, torch.float8_e4m3fn]
 EB = {torch.bfloat16: 2, torch.float16: 2, torch.float32: 4, torch.float8_e4m3fn: 1}
 
@@ -140,7 +143,7 @@ def _build(c, gpu):
     return plan, dst_cs, spans, src_o, dst_o, inv, k_scale
 
 
-@pytest.mark.parametrize("seed", range(48))
+@pytest.mark.parametrize("seed", range(max(48, _EXTRA)))
 def test_random_batched_shift_matches_oracle(gpu, seed):
     c = _case(seed)
     desc = {k: (str(v) if k == "dtype" else v) for k, v in c.items() if k != "rng"}
@@ -158,7 +161,7 @@ def test_random_batched_shift_matches_oracle(gpu, seed):
             assert np.array_equal(bits(t), dst_o.caches[g][layer]), f"group {g} layer {layer}"
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(max(24, _EXTRA // 2)))
 def test_random_single_span_matches_oracle(gpu, seed):
     """The per-layer entry point (``scatter_shifted``, the reference's signature) over
     random geometries: any element type, head size, rotary width, head count, layout and
