@@ -24,6 +24,8 @@ Prints one JSON line.  Also measured, in the same line:
   rows of its published table.
 * ``tp_shares``: the headline shift at 4, 2 and 1 KV heads (one GPU's share at TP 2, 4,
   8), bf16 and fp8.
+* ``size_sweep``: one batched shift of 512 to 32,768 tokens x 40 layers, to show where
+  the fixed cost of a call stops mattering.
 * ``ceilings``: a plain elementwise copy of the same bytes, and the headline with its
   block tables made the identity: what the GPU streams with nothing scattered.
 * ``dst_layouts``: the headline shift into fused NHD caches and into caches that keep K
@@ -365,6 +367,45 @@ def tp_shares(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def size_sweep(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: one batched shift of n tokens x 40 layers (a flat store span into
+    an HND paged cache through shuffled slots, delta 186) for n from 512 to 32,768: how
+    the fixed costs of a call (the plan kernel, two launches, ramp-up and drain) weigh
+    on small shifts."""
+    import numpy as np
+    import torch
+
+    from marathon_amd.shift_kernels import inv_freq_for
+    from marathon_amd.spans import CacheSet, ShiftPlan, span_array
+
+    layers, heads, d, bs = 40, 8, 128, 16
+    out = {}
+    for n in (512, 2048, 8192, 32768):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(n)
+        blocks = -(-n // bs) + 8
+        src = [torch.randn(n, heads, 2 * d, dtype=torch.bfloat16, device=dev, generator=gen)
+               for _ in range(layers)]
+        kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
+              for _ in range(layers)]
+        table = torch.randperm(blocks, device=dev, generator=gen)
+        pos = torch.arange(n, device=dev)
+        slot = table[pos // bs] * bs + pos % bs
+        plan = ShiftPlan(span_array([(0, 0, 0, 0, n, 186, 0, 0)]), CacheSet([src], "flat"),
+                         CacheSet([kv], "hnd", bs), inv_freq=inv_freq_for(d, 1e6),
+                         src_mode="flat", dst_mode="slots", dst_index=slot)
+        warm_up(lambda: plan.launch(stream.cuda_stream))
+        _, per = time_plan(plan, max(steps, 50), warmup, stream)
+        ms = float(np.median(per))
+        gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+        out[f"tokens_{n}"] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
+                              "frac_of_peak": round(gbs / PEAK_GBS, 4),
+                              "us_per_token": round(ms * 1e3 / n, 5)}
+        del src, kv, plan
+        torch.cuda.empty_cache()
+    return out
+
+
 def ceilings(dev, steps: int, warmup: int, stream) -> dict:
     """Informational: what this GPU streams with nothing scattered, beside the headline.
 
@@ -629,6 +670,8 @@ def main() -> int:
                     "multi-span and batched-session workloads")
     ap.add_argument("--no-tp-shares", action="store_true",
                     help="skip the timings of one GPU's share at 4, 2 and 1 KV heads")
+    ap.add_argument("--no-size-sweep", action="store_true",
+                    help="skip the batched shifts of 512 to 32,768 tokens")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the plain elementwise copy and the identity-table headline")
     ap.add_argument("--no-dst-layouts", action="store_true",
@@ -701,6 +744,9 @@ def main() -> int:
     if not args.no_tp_shares:
         log("tensor-parallel shares of the headline shift (4, 2, 1 KV heads)")
         extra["tp_shares"] = tp_shares(dev, side_steps, args.warmup, stream)
+    if not args.no_size_sweep:
+        log("size sweep: one batched shift of 512 to 32,768 tokens x 40 layers")
+        extra["size_sweep"] = size_sweep(dev, side_steps, args.warmup, stream)
     if not args.no_ceilings:
         log("ceilings: elementwise copy, the headline with identity tables")
         extra["ceilings"] = ceilings(dev, side_steps, args.warmup, stream)
