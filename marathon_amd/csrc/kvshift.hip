@@ -1000,6 +1000,8 @@ extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
     return fail(MKV_ERR_ALIGN, "src or kv base address not 16-byte aligned");
   if (!aligned16(static_cast<uint64_t>(src_token_stride * eb)))
     return fail(MKV_ERR_ALIGN, "src token stride not 16-byte aligned");
+  if (!aligned16(static_cast<uint64_t>(src_head_stride * eb)))
+    return fail(MKV_ERR_ALIGN, "src head stride not 16-byte aligned");
 
   mkv_side_t d_in{};
   d_in.index = slots;

@@ -47,13 +47,16 @@ class CacheSet:
     def __post_init__(self):
         if self.layout not in ("flat", "hnd", "nhd"):
             raise ValueError(f"layout {self.layout!r}")
-        if not self.caches or not self.caches[0]:
-            raise ValueError("empty CacheSet")
-        if isinstance(self.caches[0], torch.Tensor):
+        # a flat list of per-layer tensors is one group; wrap it before any truth test,
+        # since a tensor has no truth value
+        if len(self.caches) and isinstance(self.caches[0], torch.Tensor):
             self.caches = [list(self.caches)]
+        if self.v_caches is not None and len(self.v_caches) and isinstance(
+                self.v_caches[0], torch.Tensor):
+            self.v_caches = [list(self.v_caches)]
+        if len(self.caches) == 0 or len(self.caches[0]) == 0:
+            raise ValueError("empty CacheSet")
         if self.v_caches is not None:
-            if isinstance(self.v_caches[0], torch.Tensor):
-                self.v_caches = [list(self.v_caches)]
             if len(self.v_caches) != len(self.caches) or any(
                     len(kr) != len(vr) for kr, vr in zip(self.caches, self.v_caches)):
                 raise ValueError("v_caches must match caches group by group, layer by layer")

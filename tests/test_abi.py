@@ -112,6 +112,8 @@ def test_host_side_argument_errors_need_no_gpu():
     assert _scatter(dtype=_lib.MKV_FP8_E4M3, scale=None) == _lib.MKV_ERR_ARG
     assert _scatter(src=(1 << 20) + 8) == _lib.MKV_ERR_ALIGN
     assert _scatter(sts=2047) == _lib.MKV_ERR_ALIGN
+    assert _scatter(shs=252) == _lib.MKV_ERR_ALIGN  # a 504-byte head stride
+    assert b"head stride" in lib.mkv_last_error()
     # the reference returns early on an empty load (shift_kernels.py:185-186)
     assert _scatter(n=0) == _lib.MKV_OK
     assert lib.mkv_last_error() == b""
@@ -188,3 +190,20 @@ def test_cacheset_split_planes_are_validated_and_sized():
                                                                 dtype=torch.bfloat16)]])
     with pytest.raises(ValueError, match="group by group"):
         CacheSet([k], "nhd", 16, v_caches=[v[:2]])
+
+
+def test_cacheset_takes_a_flat_list_of_layers():
+    """A flat list of per-layer tensors is one group, in every layout."""
+    from marathon_amd.spans import CacheSet
+
+    flat = CacheSet([torch.zeros(64, 8, 256) for _ in range(2)], "flat")
+    assert (flat.groups, flat.layers, flat.heads, flat.head_size) == (1, 2, 8, 128)
+    hnd = CacheSet([torch.zeros(4, 8, 16, 256)], "hnd", 16)
+    assert (hnd.groups, hnd.layers, hnd.block_size) == (1, 1, 16)
+    k = [torch.zeros(4, 16, 8, 128)]
+    split = CacheSet(k, "nhd", 16, v_caches=[torch.zeros(4, 16, 8, 128)])
+    assert (split.groups, split.split, split.head_size) == (1, True, 128)
+    with pytest.raises(ValueError, match="empty"):
+        CacheSet([], "flat")
+    with pytest.raises(ValueError, match="empty"):
+        CacheSet([[]], "flat")
