@@ -5,13 +5,11 @@
 // nearest even, and its NaN code is 0xFF where the format's canonical NaN is 0x7F, so
 // callers rewrite NaN lanes to 0x7F.
 //
-// quant(): y / scale through Markstein's correction, q0 = RN(y * r),
-// q = fma(fma(-q0, scale, y), r, q0) with r = RN(1 / scale).  It equals the correctly
-// rounded quotient for every fp32 y with 2^-12 <= |y / scale| < 2^10 at scales in
-// [0.01, 0.1] (checked exhaustively on the CPU); smaller quotients encode to a signed
-// zero either way, larger ones cannot occur.  copysign keeps -0 / scale = -0.  The
-// result is clamped to +-448 with IEEE minNum/maxNum, which turn a NaN into 448: callers
-// that can see NaN inputs rewrite those bytes.
+// quant(): the correctly rounded IEEE quotient y / scale (the compiler's fp32 division,
+// which is correctly rounded for HIP device code unless fast-math options are given),
+// for every fp32 y and every scale, with no precondition on either.  The result is
+// clamped to +-448 with IEEE minNum/maxNum, which turn a NaN into 448: callers that can
+// see NaN inputs rewrite those bytes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -40,12 +38,8 @@ __device__ __forceinline__ float clamp448(float q) {
   return __builtin_fmaxf(__builtin_fminf(q, 448.0f), -448.0f);
 }
 
-// clamp(RN(y / scale)); rcp must be RN(1 / scale).
-__device__ __forceinline__ float quant(float y, float scale, float rcp) {
-  const float q0 = y * rcp;
-  const float r = __builtin_fmaf(-q0, scale, y);
-  return clamp448(__builtin_copysignf(__builtin_fmaf(r, rcp, q0), y));
-}
+// clamp(RN(y / scale)).
+__device__ __forceinline__ float quant(float y, float scale) { return clamp448(y / scale); }
 
 // Four in-range floats to four codes (round to nearest even), low byte first.
 __device__ __forceinline__ uint32_t encode4(const float* q) {

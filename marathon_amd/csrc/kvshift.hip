@@ -306,7 +306,7 @@ struct Rotor;
 template <>
 struct Rotor<MKV_BF16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -323,7 +323,7 @@ struct Rotor<MKV_BF16> {
 template <>
 struct Rotor<MKV_F16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -340,7 +340,7 @@ struct Rotor<MKV_F16> {
 template <>
 struct Rotor<MKV_F32> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -357,7 +357,7 @@ struct Rotor<MKV_F32> {
 template <>
 struct Rotor<MKV_FP8_E4M3> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float scale, float rcp) {
+                                              const float* s, float scale) {
     using namespace mkv_fp8;
     u32x4 out;
 #pragma unroll
@@ -368,7 +368,7 @@ struct Rotor<MKV_FP8_E4M3> {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int e = 4 * w + b;
-        q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale, rcp);
+        q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale);
       }
       out[w] = encode4(q);
     }
@@ -612,7 +612,6 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       if (p.rotary > 0) scale = ld_const(p.k_scale + layer);
     }
   }
-  const float rcp = 1.0f / scale;  // correctly rounded (fp8 requantisation)
 
   for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
     // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
@@ -775,7 +774,7 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
             cur_span = span_u[u];
           }
         }
-        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale, rcp);
+        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale);
       }
     }
 

@@ -20,6 +20,24 @@ def rope_emb_tables(delta: int, inv_freq: torch.Tensor) -> tuple[torch.Tensor, t
     return emb.cos(), emb.sin()
 
 
+def rope_shift_tables(delta: int, head_size: int, inv_freq: torch.Tensor, device) -> dict:
+    """The reference's ``rope_shift`` tables built with torch on ``device``
+    (shift_kernels.py:68-84): ``cos``/``sgn`` [head_size] as its Triton kernel reads them
+    and ``emb_cos``/``emb_sin`` [rotary] as its torch path reads them."""
+    rotary = 2 * int(inv_freq.numel())
+    assert rotary <= head_size, f"rotary {rotary} > head_size {head_size}"
+    half = rotary // 2
+    ang = float(delta) * inv_freq.to(device=device, dtype=torch.float32)
+    emb = torch.cat((ang, ang))
+    cos = torch.ones(head_size, dtype=torch.float32, device=device)
+    cos[:rotary] = emb.cos()
+    sin = emb.sin()
+    sgn = torch.zeros(head_size, dtype=torch.float32, device=device)
+    sgn[:half] = -sin[:half]
+    sgn[half:rotary] = sin[half:rotary]
+    return {"cos": cos, "sgn": sgn, "emb_cos": emb.cos(), "emb_sin": sin}
+
+
 def shift_into_paged(
     rows: torch.Tensor,
     cache: torch.Tensor,

@@ -68,6 +68,34 @@ def test_bf16_matches_oracle_and_reference_path(gpu, delta, hnd, n):
     assert float((ulp_bf16(got, ref_bits) > 1).mean()) < 1e-3
 
 
+@pytest.mark.parametrize("tables_on", ["cpu", "gpu"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hnd", [True, False])
+def test_reference_tables_reproduce_the_reference_path_bit_for_bit(gpu, tables_on, dtype, hnd):
+    """The drop-in as a caller keeping the reference's ``rope_shift`` would use it: the
+    reference's own tables (torch fp32 cos/sin, built on the CPU or, as the connector
+    builds them, on the GPU; shift_kernels.py:68-84) through ``mkv_scatter_shifted``
+    give exactly the bits of the reference's torch op sequence with the same tables
+    (shift_kernels.py:141-159): 0 ulp, every element, every delta."""
+    from marathon_amd import RopeShift
+
+    inv = inv_freq()
+    for n, delta in ((64, -3000), (37, -4), (64, 4), (37, 186), (64, 10000), (37, -566)):
+        print(f"case reference tables on {tables_on} {dtype} hnd={hnd} n={n} delta={delta}",
+              flush=True)
+        src, kv, slots = _case(abs(delta) + n, n, hnd, dtype)
+        t = torch_path.rope_shift_tables(delta, 128, inv, "cpu" if tables_on == "cpu" else gpu)
+        shift = RopeShift(delta, t["cos"].to(gpu), t["sgn"].to(gpu), None, t["emb_cos"],
+                          t["emb_sin"], inv.to(gpu), 128)
+        got = bits(_run_gpu(gpu, src, kv, slots, 16, hnd, shift))
+        ref = kv.clone()
+        torch_path.shift_into_paged(src, ref, slots, 16, hnd,
+                                    (t["emb_cos"].cpu(), t["emb_sin"].cpu()))
+        want = bits(ref)
+        assert np.array_equal(got, want), (
+            f"{int((got != want).sum())} of {want.size} elements differ from the torch path")
+
+
 def test_zero_length_load_is_a_noop(gpu):
     kv = torch.randn(4, 8, 16, 256, dtype=torch.bfloat16, device=gpu)
     before = kv.clone()
