@@ -14,8 +14,9 @@ Prints one JSON line.  Also measured, in the same line:
   FETCH_SIZE/WRITE_SIZE profile of this kernel and workload, when present.
 * ``cpu_baseline``: the reference's torch shift path (its op sequence, restated in
   ``oracle/torch_path.py``) on the host CPU over the headline workload itself (all 40
-  layers and 8 spans), best of 3 after a warm-up; the Qwen3-0.6B-shaped CPU case
-  (28 layers x 4,096 tokens, delta +37) is reported beside it.
+  layers and 8 spans), best of 5 after a warm-up, on every CPU the process may use; the
+  Qwen3-0.6B-shaped CPU case (28 layers x 4,096 tokens, delta +37) is reported beside
+  it, with the HIP path's time for that same shift (``qwen3_0_6b_shift_hip``).
 * ``reference_shape``: the reference benchmark's own shape (30,720 tokens x 40 layers,
   delta 186, flat store -> HND paged cache, scattered block table), for comparison with
   its published 6.54 ms on an RTX 5090, as one batched launch.
@@ -130,15 +131,32 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(reps: int = 3) -> dict:
+def host_cores() -> dict:
+    """CPUs this process may run on (its affinity set), next to what the OS reports."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"os_cpu_count": os.cpu_count(), "usable": usable}
+
+
+def cpu_baseline(reps: int = 5, gpu_small: dict | None = None) -> dict:
     """The reference torch shift path on the host CPU, on the headline workload itself:
     the Qwen3-14B multi-span shift (40 layers, 8 spans, 22,141 tokens), every layer and
     every span, read from the reference's flat store (shift_store.py:225-236, rows of a
     span are one contiguous view) and scattered into an HND paged cache through its
     slots.  Best of ``reps`` passes after one warm-up pass; also the Qwen3-0.6B case
-    (28 layers x 4,096 tokens, delta +37), the reference's own CPU-sized shift."""
+    (28 layers x 4,096 tokens, delta +37), the reference's own CPU-sized shift, with
+    the HIP path's time for the same shift (``gpu_small``) beside it.
+
+    torch runs on every CPU this process may use (its affinity set; equal to
+    ``os.cpu_count()`` unless the process is confined to fewer), as the reference's
+    benchmark protocol asks (``torch.set_num_threads`` before timing)."""
     import numpy as np
     import torch
+
+    cores = host_cores()
+    torch.set_num_threads(cores["usable"])
 
     from marathon_amd import workloads as W
     from marathon_amd.shift_kernels import inv_freq_for
@@ -184,21 +202,92 @@ def cpu_baseline(reps: int = 3) -> dict:
         if i:
             best_small = min(best_small, dt)
     moved_small = 2 * sum(t.numel() * t.element_size() for t in small["src"])
+    small_row = {
+        "GB_s": round(moved_small / best_small / 1e9, 3),
+        "ms_per_shift": round(best_small * 1e3, 2),
+    }
+    if gpu_small:
+        small_row["hip"] = gpu_small
+        small_row["hip_speedup_batched"] = round(best_small * 1e3 / gpu_small["batched_ms"], 1)
     return {
         "value": round(moved / best / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "os_cpu_count": cores["os_cpu_count"],
+        "usable_cpus": cores["usable"],
         "kind": "port",
         "sample": f"the reference torch shift path (oracle/torch_path.py) on the CPU over the "
         f"whole Qwen3-14B multi-span shift: {layers} layers x 8 spans, {tokens:,} tokens, flat "
         f"store -> HND paged cache; best of {reps} passes after 1 warm-up; "
-        f"{best * 1e3:.1f} ms per shift; CPU: {_cpu_model()}",
+        f"{best * 1e3:.1f} ms per shift; {torch.get_num_threads()} torch threads "
+        f"(os.cpu_count() {cores['os_cpu_count']}, {cores['usable']} usable); "
+        f"CPU: {_cpu_model()}",
         "ms_per_shift": round(best * 1e3, 2),
-        "qwen3_0_6b_4096_tokens": {
-            "GB_s": round(moved_small / best_small / 1e9, 3),
-            "ms_per_shift": round(best_small * 1e3, 2),
-        },
+        "qwen3_0_6b_4096_tokens": small_row,
     }
+
+
+def qwen3_0_6b_hip(dev, steps: int, warmup: int, stream, iters: int = 5) -> dict:
+    """The Qwen3-0.6B-shaped shift the CPU baseline also times (28 layers, a flat store of
+    4,096 tokens per layer, one span shifted by +37 into 259 of 512 seeded HND blocks),
+    on the HIP path: one batched launch (HIP events on the launch stream, mean over
+    ``steps``) and the reference's call pattern of 28 per-layer ``scatter_shifted``
+    calls (host wall clock, best of ``iters``).  A sampled row is checked against the
+    oracle."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+    from marathon_amd.shift_kernels import rope_shift, scatter_shifted
+    from marathon_amd.spans import CacheSet, ShiftPlan, span_array
+    from oracle import kvshift_oracle as orc
+
+    wl = W.qwen3_0_6b_cpu_shift()
+    delta, n = wl["delta"], wl["src"][0].shape[0]
+    src = [t.to(dev) for t in wl["src"]]
+    kv = [t.to(dev) for t in wl["kv"]]
+    slots = wl["slots"].to(dev)
+    plan = ShiftPlan(span_array([(0, 0, 0, 0, n, delta, 0, 0)]), CacheSet(src, "flat"),
+                     CacheSet(kv, "hnd", 16), inv_freq=wl["inv_freq"], src_mode="flat",
+                     dst_mode="slots", dst_index=wl["slots"])
+    warm_up(lambda: plan.launch(stream.cuda_stream))
+    _, per = time_plan(plan, max(steps, 50), warmup, stream)
+    ms = float(np.mean(per))
+    shift = rope_shift(delta, 128, wl["inv_freq"], dev)
+
+    def loop():
+        for s_, k_ in zip(src, kv):
+            scatter_shifted(s_, k_, slots, 16, True, shift)
+
+    warm_up(loop)
+    best = float("inf")
+    for _ in range(iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loop()
+        torch.cuda.synchronize()
+        best = min(best, (time.perf_counter() - t0) * 1e3)
+    t = int(np.random.default_rng(1).integers(n))
+    slot = int(wl["slots"][t])
+    sb = wl["src"][-1][t].view(torch.int16).numpy().view(np.uint16)
+    gb = kv[-1][slot // 16, :, slot % 16].cpu().view(torch.int16).numpy().view(np.uint16)
+    if not (np.array_equal(gb[:, :128], orc.rotate_k_bits(sb[:, :128], delta,
+                                                         wl["inv_freq"].numpy(), "bf16"))
+            and np.array_equal(gb[:, 128:], sb[:, 128:])):
+        raise AssertionError("Qwen3-0.6B shift differs from the oracle")
+    moved = plan.algorithmic_bytes
+    out = {
+        "shape": "28 layers x 4,096 tokens x 8 heads x 128, bf16, delta +37, flat store -> "
+        "HND paged (259 of 512 seeded blocks)",
+        "bytes": moved,
+        "batched_ms": round(ms, 4),
+        "batched_GB_s": round(moved / (ms / 1e3) / 1e9, 1),
+        "per_layer_loop_ms": round(best, 4),
+        "per_layer_loop_GB_s": round(moved / (best / 1e3) / 1e9, 1),
+    }
+    del src, kv, plan
+    torch.cuda.empty_cache()
+    return out
 
 
 def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
@@ -758,10 +847,12 @@ def main() -> int:
         extra["connector_step"] = connector_step(dev, side_steps, args.warmup)
         log("connector save step (paged -> block store)")
         extra["save_step"] = save_step(dev, side_steps, args.warmup)
+    log("Qwen3-0.6B shift on the HIP path (the CPU baseline's small case)")
+    small = qwen3_0_6b_hip(dev, side_steps, args.warmup, stream)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (reference torch path on the host, the Qwen3-14B multi-span shift)")
-        cpu = cpu_baseline()
+        cpu = cpu_baseline(gpu_small=small)
 
     tokens = int(bytes_step // (2 * 40 * 8 * 256 * 2))
     line = {
@@ -800,6 +891,7 @@ def main() -> int:
             "kernel_ms": round(ev_ms, 4),
         },
         "cpu_baseline": cpu,
+        "qwen3_0_6b_shift_hip": small,
         "parity": f"{checked} sampled rows bit-identical to the oracle after timing",
         **extra,
     }

@@ -35,6 +35,11 @@
  * per-layer scale, rotates in fp32 and requantises:
  *     x = fl32(decode(code) * k_scale[layer]);   y = rotation of x as above;
  *     q = e4m3fn_RNE(clamp(fl32(y / k_scale[layer]), -448, 448))   (NaN -> 0x7F)
+ * The quotient is evaluated with Markstein's correction (marathon_amd/csrc/fp8_e4m3.h);
+ * it equals the correctly rounded fl32(y / k_scale) for every y that can change a code
+ * at every scale checked exhaustively (every K scale of this library's fp8 workloads and
+ * tests) and on 3e8 random pairs over 41 binades of scale; other scales are covered by
+ * that random sample only.
  * V bytes are copied raw for every element type.
  */
 #ifndef MARATHON_KVSHIFT_H

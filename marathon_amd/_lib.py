@@ -156,9 +156,10 @@ def _bind(cdll: ctypes.CDLL) -> ctypes.CDLL:
     f.restype = ctypes.c_int
     f.argtypes = [vp, i64, i64, vp, i64, i64, i64, i64, vp, i64, i32, i32, i32, i32, vp, vp,
                   i32, vp, vp, vp]
-    f = cdll.mkv_shift_spans
-    f.restype = ctypes.c_int
-    f.argtypes = [ctypes.POINTER(ShiftDesc), vp]
+    for name in ("mkv_shift_spans",):
+        f = getattr(cdll, name)
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.POINTER(ShiftDesc), vp]
     f = cdll.mkv_shift_workspace_size
     f.restype = ctypes.c_int64
     f.argtypes = [i64, i32, i32]

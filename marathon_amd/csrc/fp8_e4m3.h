@@ -5,11 +5,18 @@
 // nearest even, and its NaN code is 0xFF where the format's canonical NaN is 0x7F, so
 // callers rewrite NaN lanes to 0x7F.
 //
-// quant(): the correctly rounded IEEE quotient y / scale (the compiler's fp32 division,
-// which is correctly rounded for HIP device code unless fast-math options are given),
-// for every fp32 y and every scale, with no precondition on either.  The result is
-// clamped to +-448 with IEEE minNum/maxNum, which turn a NaN into 448: callers that can
-// see NaN inputs rewrite those bytes.
+// quant(): y / scale through Markstein's correction, q0 = RN(y * r),
+// q = fma(fma(-q0, scale, y), r, q0) with r = RN(1 / scale): three VALU operations where
+// the compiler's correctly rounded division takes about ten (measured 8% slower on the
+// fp8 Qwen3-14B shift).  Markstein's theorem makes q the correctly rounded quotient
+// whenever q0 is within one ulp of y / scale.  Checked exhaustively on the CPU: q equals
+// RN(y / scale) for every fp32 y with 2^-12 <= |y / scale| < 2^10 (the quotients that
+// can change an e4m3fn code) at every K scale of the fp8 workloads and GPU tests, and on
+// 3e8 random pairs with scales over 41 binades; other scales are checked only by that
+// random sample.  Smaller quotients encode to a signed zero either way, larger ones
+// clamp.  copysign keeps -0 / scale = -0.  The result is clamped to +-448 with IEEE
+// minNum/maxNum, which turn a NaN into 448: callers that can see NaN inputs rewrite
+// those bytes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,8 +45,12 @@ __device__ __forceinline__ float clamp448(float q) {
   return __builtin_fmaxf(__builtin_fminf(q, 448.0f), -448.0f);
 }
 
-// clamp(RN(y / scale)).
-__device__ __forceinline__ float quant(float y, float scale) { return clamp448(y / scale); }
+// clamp(RN(y / scale)); rcp must be RN(1 / scale).
+__device__ __forceinline__ float quant(float y, float scale, float rcp) {
+  const float q0 = y * rcp;
+  const float r = __builtin_fmaf(-q0, scale, y);
+  return clamp448(__builtin_copysignf(__builtin_fmaf(r, rcp, q0), y));
+}
 
 // Four in-range floats to four codes (round to nearest even), low byte first.
 __device__ __forceinline__ uint32_t encode4(const float* q) {

@@ -306,7 +306,7 @@ struct Rotor;
 template <>
 struct Rotor<MKV_BF16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float) {
+                                              const float* s, float, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -323,7 +323,7 @@ struct Rotor<MKV_BF16> {
 template <>
 struct Rotor<MKV_F16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float) {
+                                              const float* s, float, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -340,7 +340,7 @@ struct Rotor<MKV_F16> {
 template <>
 struct Rotor<MKV_F32> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float) {
+                                              const float* s, float, float) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -357,7 +357,7 @@ struct Rotor<MKV_F32> {
 template <>
 struct Rotor<MKV_FP8_E4M3> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float scale) {
+                                              const float* s, float scale, float rcp) {
     using namespace mkv_fp8;
     u32x4 out;
 #pragma unroll
@@ -368,7 +368,7 @@ struct Rotor<MKV_FP8_E4M3> {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int e = 4 * w + b;
-        q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale);
+        q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale, rcp);
       }
       out[w] = encode4(q);
     }
@@ -612,6 +612,7 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       if (p.rotary > 0) scale = ld_const(p.k_scale + layer);
     }
   }
+  const float rcp = 1.0f / scale;  // correctly rounded (fp8 requantisation)
 
   for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
     // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
@@ -774,7 +775,7 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
             cur_span = span_u[u];
           }
         }
-        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale);
+        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale, rcp);
       }
     }
 
@@ -1065,10 +1066,13 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
       d->dst.v_base == nullptr)
     return fail(MKV_ERR_ARG, "NULL base-address table");
   const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary);
-  if (d->workspace == nullptr || d->workspace_bytes < need)
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws_ptr = d->workspace;
+  const int64_t ws_bytes = d->workspace_bytes;
+  if (ws_ptr == nullptr || ws_bytes < need)
     return fail(MKV_ERR_ARG, "workspace of %lld bytes needed (mkv_shift_workspace_size)",
                 (long long)need);
-  if (!aligned16(reinterpret_cast<uint64_t>(d->workspace)))
+  if (!aligned16(reinterpret_cast<uint64_t>(ws_ptr)))
     return fail(MKV_ERR_ALIGN, "workspace not 16-byte aligned");
   const int64_t tiles = (d->total_tokens + g.tile_tokens - 1) / g.tile_tokens;
   if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "total_tokens too large");
@@ -1080,7 +1084,7 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
   if (rc != MKV_OK) return rc;
   rc = make_side(d->dst, eb, pp.dst, dst_hs, "dst");
   if (rc != MKV_OK) return rc;
-  char* ws = static_cast<char*>(d->workspace);
+  char* ws = static_cast<char*>(ws_ptr);
   float* tables = reinterpret_cast<float*>(ws);
   TokRec* recs = reinterpret_cast<TokRec*>(
       ws + align256(static_cast<int64_t>(d->n_spans) * 2 * d->rotary *
@@ -1101,7 +1105,6 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
   if (plan_grid > 4096) plan_grid = 4096;
   if (plan_grid < 1) plan_grid = 1;
   const size_t lds = sizeof(int64_t) * (static_cast<size_t>(d->n_spans) + 1);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kPlanThreads), lds,
                      st, pp);
   hipError_t e = hipGetLastError();

@@ -174,6 +174,14 @@ class Workload:
         return 2 * self.tokens * self.layers * self.dst.heads * 2 * self.dst.head_size * eb
 
 
+def fp8_layer_scales(seed: int, layers: int) -> tuple[np.ndarray, np.ndarray]:
+    """Per-layer fp32 K and V scales of an fp8 workload, uniform in [0.01, 0.1]."""
+    srng = np.random.default_rng(seed)
+    k = srng.uniform(0.01, 0.1, layers).astype(np.float32)
+    v = srng.uniform(0.01, 0.1, layers).astype(np.float32)
+    return k, v
+
+
 def _randn_cache(shape, dtype, gen, device, scale=None) -> torch.Tensor:
     if dtype == torch.float8_e4m3fn:
         x = torch.randn(shape, dtype=torch.float32, device=device, generator=gen)
@@ -212,9 +220,8 @@ def single_session_workload(
     dst_table = rng.permutation(dst_pool)[:dst_need].astype(np.int64)
     k_scale = v_scale = None
     if dtype == torch.float8_e4m3fn:
-        srng = np.random.default_rng(scale_seed if scale_seed is not None else seed)
-        k_scale = torch.from_numpy(srng.uniform(0.01, 0.1, layers).astype(np.float32))
-        v_scale = torch.from_numpy(srng.uniform(0.01, 0.1, layers).astype(np.float32))
+        k, v = fp8_layer_scales(scale_seed if scale_seed is not None else seed, layers)
+        k_scale, v_scale = torch.from_numpy(k), torch.from_numpy(v)
     src_caches, dst_caches = [], []
     for layer in range(layers):
         if dtype == torch.float8_e4m3fn:

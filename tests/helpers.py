@@ -55,3 +55,19 @@ def oracle_spans(spans: np.ndarray) -> list:
 
 def ulp_bf16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return orc.ulp_distance_bf16(a, b)
+
+
+def within_table_rounding(got: np.ndarray, ref: np.ndarray, src_k: np.ndarray,
+                          rotary: int) -> np.ndarray:
+    """Per element: ``got`` (correctly rounded cos/sin tables) and ``ref`` (the reference's
+    torch fp32 tables, each within 1 fp32 ulp of them) differ by at most 1 bf16 ulp plus
+    what the tables' rounding can move ``k*c + kp*s`` before the cast: 2 * (|k| + |kp|) *
+    2^-24.  Where the two products nearly cancel, that term exceeds 1 ulp of the small
+    result; everywhere else the bound is 1 ulp.  All arrays are bf16 bits ``[..., D]``."""
+    g = orc.bf16_to_f32(got[..., :rotary]).astype(np.float64)
+    r = orc.bf16_to_f32(ref[..., :rotary]).astype(np.float64)
+    k = orc.bf16_to_f32(src_k[..., :rotary]).astype(np.float64)
+    kp = np.roll(k, rotary // 2, axis=-1)
+    big = np.maximum(np.abs(g), np.abs(r)).astype(np.float32)
+    ulp = np.spacing(big).astype(np.float64) * 65536.0  # bf16 keeps 8 of fp32's 24 bits
+    return np.abs(g - r) <= ulp + 2.0 * (np.abs(k) + np.abs(kp)) * 2.0**-24

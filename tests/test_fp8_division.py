@@ -1,0 +1,64 @@
+"""The fp8 requantisation's division, checked exhaustively on the CPU.
+
+The kernel computes y / k_scale with Markstein's correction (two fmas after a multiply
+by the rounded reciprocal; marathon_amd/csrc/fp8_e4m3.h) and relies on it equalling the
+correctly rounded quotient, which the oracle computes by an IEEE division.  An IEEE
+division in the kernel measured 8% slower on the fp8 Qwen3-14B shift, so the kernel
+keeps Markstein and this test walks, at every K scale the fp8 workloads and the GPU
+tests use, every fp32 y whose quotient can change an e4m3fn code (2^-12 <= |y/s| <
+2^10, both signs: 3.7e8 quotients per scale), plus 3e8 random (scale, y) pairs over 41
+binades of scale.  tests/fp8_division_check.c does the walking.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from marathon_amd import workloads as W
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+# fixed K scales of the fp8 GPU tests (tests/test_gpu_spans.py, test_gpu_fp8_codec.py)
+# and both ends of the range the random ones are drawn from
+TEST_SCALES = [0.01, 0.1, 0.021, 0.031, 0.037, 0.044, 0.05, 0.066, 0.072, 0.081]
+
+
+def _hex(scales) -> list:
+    return [f"{int(b):08x}" for b in np.asarray(scales, np.float32).view(np.uint32)]
+
+
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    exe = str(tmp_path_factory.mktemp("fp8div") / "fp8_division_check")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math",
+                    os.path.join(HERE, "fp8_division_check.c"), "-o", exe, "-lm", "-lpthread"],
+                   check=True)
+    return exe
+
+
+def _run(exe, args, timeout=600):
+    out = subprocess.run([exe, *args], capture_output=True, text=True, timeout=timeout)
+    assert out.returncode == 0, out.stdout[-2000:]
+    assert out.stdout.strip().endswith(" 0 mismatches"), out.stdout[-2000:]
+    return out.stdout
+
+
+def test_every_k_scale_of_the_fp8_qwen3_14b_workload(checker):
+    k_scale, _ = W.fp8_layer_scales(4, 40)  # the fp8 multi-span shift's 40 layers
+    out = _run(checker, _hex(k_scale))
+    assert out.count("scale ") == 40
+
+
+def test_the_fixed_scales_of_the_fp8_gpu_tests(checker):
+    _run(checker, _hex(TEST_SCALES))
+
+
+def test_random_scales_over_41_binades(checker):
+    _run(checker, ["random", "300000000"])

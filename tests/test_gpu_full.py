@@ -20,7 +20,7 @@ from marathon_amd import workloads as W
 from marathon_amd.spans import CacheSet, ShiftPlan, span_array
 from oracle import fast_rotate as fast
 from oracle import kvshift_oracle as orc
-from tests.helpers import bits, ulp_bf16
+from tests.helpers import bits, ulp_bf16, within_table_rounding
 
 pytestmark = pytest.mark.gpu
 
@@ -62,6 +62,11 @@ def _check_full(wl, dtype_name, snapshot=True, threads=16):
     wl.plan().launch(error_flags=flags)
     torch.cuda.synchronize(dev)
     assert int(flags.item()) == 0
+    _compare_full(wl, dtype_name, snapshot, threads)
+
+
+def _compare_full(wl, dtype_name, snapshot, threads):
+    dev = wl.dst.first.device
     spans = wl.spans
     src_side = orc.Side(None, "nhd", 16, wl.src_mode, wl.src_index.numpy())
     dst_side = orc.Side(None, "hnd", 16, wl.dst_mode, wl.dst_index.numpy())
@@ -228,8 +233,13 @@ def test_qwen3_0_6b_shift_through_both_entry_points(gpu):
     seeded blocks of an HND cache.  Run through the HIP path twice -- 28 per-layer
     ``scatter_shifted`` launches (the reference connector's call pattern,
     vllm_shift_connector.py:505-518) and one batched ``mkv_shift_spans`` launch -- and
-    every byte of every layer's cache is compared with the oracle; K is also within 1
-    bf16 ulp of the reference's torch op sequence (oracle/torch_path.py)."""
+    every byte of every layer's cache is compared with the oracle.  Against the
+    reference's torch op sequence with torch's own tables (oracle/torch_path.py), K is
+    within 1 bf16 ulp except where the rotation's two products nearly cancel, and there
+    within what the tables' 1-fp32-ulp difference can move the sum; the reference
+    test's own bounds hold (max error <= 2^-7 max|src|, < 0.1% of elements beyond
+    1 ulp).  With the reference's own tables the kernel reproduces that sequence bit
+    for bit (tests/test_gpu_scatter.py)."""
     from marathon_amd import rope_shift, scatter_shifted
     from oracle import torch_path
 
@@ -256,6 +266,7 @@ def test_qwen3_0_6b_shift_through_both_entry_points(gpu):
     plan.launch(error_flags=flags)
     torch.cuda.synchronize(gpu)
     assert int(flags.item()) == 0
+    beyond, worst_abs, src_max = 0, 0.0, 0.0
     for layer in range(layers):
         sb = bits(wl["src"][layer])
         want = bits(wl["kv"][layer])
@@ -268,4 +279,11 @@ def test_qwen3_0_6b_shift_through_both_entry_points(gpu):
         ref = wl["kv"][layer].clone()
         torch_path.shift_into_paged(wl["src"][layer], ref, slots, 16, True,
                                     torch_path.rope_emb_tables(delta, inv))
-        assert int(ulp_bf16(bits(ref), want).max()) <= 1
+        got_k, ref_k = want[blk, :, off][..., :D], bits(ref)[blk, :, off][..., :D]
+        beyond += int((ulp_bf16(got_k, ref_k) > 1).sum())
+        assert bool(within_table_rounding(got_k, ref_k, sb[..., :D], D).all()), layer
+        worst_abs = max(worst_abs, float(np.abs(orc.bf16_to_f32(got_k) - orc.bf16_to_f32(ref_k)).max()))
+        src_max = max(src_max, float(np.abs(orc.bf16_to_f32(sb)).max()))
+    # the reference test's own bounds (tests/test_shift_kernels.py:75-78)
+    assert worst_abs <= 2**-7 * src_max
+    assert beyond / (layers * 4096 * 8 * D) < 1e-3
