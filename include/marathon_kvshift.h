@@ -206,6 +206,24 @@ int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_h
  */
 int mkv_shift_spans(const mkv_shift_desc_t* desc, void* stream);
 
+/*
+ * mkv_shift_spans without a workspace argument: the same shift, the same checks and the
+ * same results, with its workspace in a library-owned device buffer of
+ * MKV_NOALLOC_SCRATCH_BYTES on each GPU (held from the library's first use on that GPU
+ * until the process ends).  desc->workspace and desc->workspace_bytes are ignored.
+ * No counterpart in the reference: this entry point is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it allocates nothing and calls no allocating routine.
+ *   - A shift whose mkv_shift_workspace_size() exceeds MKV_NOALLOC_SCRATCH_BYTES is
+ *     refused with MKV_ERR_UNSUPPORTED before anything is enqueued.
+ *   - `stream` must belong to the current device (MKV_ERR_ARG otherwise).
+ *   - Every call on one GPU shares that GPU's buffer, which keeps the last call's
+ *     contents: calls that overlap on one GPU (on different streams, or from different
+ *     threads without ordering) race.  Calls ordered on one stream do not.
+ */
+int mkv_shift_spans_noalloc(const mkv_shift_desc_t* desc, void* stream);
+#define MKV_NOALLOC_SCRATCH_BYTES (16LL << 20)
+
 /* Workspace bytes mkv_shift_spans needs for these sizes (-1 on negative input). */
 int64_t mkv_shift_workspace_size(int64_t total_tokens, int32_t n_spans, int32_t rotary);
 
@@ -214,7 +232,7 @@ const char* mkv_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. */
 int32_t mkv_abi_version(void);
-#define MKV_ABI_VERSION ((2 << 16) | 0)
+#define MKV_ABI_VERSION ((2 << 16) | 1)
 
 #ifdef __cplusplus
 }

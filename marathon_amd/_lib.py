@@ -42,7 +42,8 @@ MKV_ADDR_TABLE = 2
 
 MKV_MAX_SPANS = 4096
 MKV_MAX_HEAD_SIZE = 512
-MKV_ABI_VERSION = (2 << 16) | 0
+MKV_ABI_VERSION = (2 << 16) | 1
+MKV_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 ERROR_NAMES = {
     MKV_ERR_ARG: "MKV_ERR_ARG",
@@ -56,6 +57,7 @@ ERROR_NAMES = {
 EXPORTED = (
     "mkv_scatter_shifted",
     "mkv_shift_spans",
+    "mkv_shift_spans_noalloc",
     "mkv_shift_workspace_size",
     "mkv_last_error",
     "mkv_abi_version",
@@ -156,7 +158,7 @@ def _bind(cdll: ctypes.CDLL) -> ctypes.CDLL:
     f.restype = ctypes.c_int
     f.argtypes = [vp, i64, i64, vp, i64, i64, i64, i64, vp, i64, i32, i32, i32, i32, vp, vp,
                   i32, vp, vp, vp]
-    for name in ("mkv_shift_spans",):
+    for name in ("mkv_shift_spans", "mkv_shift_spans_noalloc"):
         f = getattr(cdll, name)
         f.restype = ctypes.c_int
         f.argtypes = [ctypes.POINTER(ShiftDesc), vp]

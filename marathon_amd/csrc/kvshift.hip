@@ -45,6 +45,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "fp8_e4m3.h"
 #include "marathon_kvshift.h"
 
@@ -956,6 +958,55 @@ int64_t workspace_bytes(int64_t total_tokens, int32_t n_spans, int32_t rotary) {
 
 }  // namespace
 
+// ------------------------------------------------------------ no-allocation scratch
+//
+// The workspace of mkv_shift_spans_noalloc: one array per GPU, in the code object's
+// device memory, held from the library's first use on that GPU until the process ends.
+// Host code never passes `scratch` itself to a kernel (on the host its name is only a
+// handle): each device's address comes from hipGetSymbolAddress, resolved once per
+// device with that device current, and that address is what the kernels receive.
+// Nothing in it needs clearing: the plan kernel writes every record and table entry the
+// shift kernel of the same call reads.
+
+__device__ __align__(256) unsigned char scratch[MKV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, once resolved
+
+// This call's scratch address: the current device's copy, which must also be the
+// device of `st` (a NULL stream is the current device's).
+int scratch_of(hipStream_t st, void** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return fail(MKV_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (st != nullptr) {
+    hipDevice_t sd = -1;
+    e = hipStreamGetDevice(st, &sd);
+    if (e != hipSuccess)
+      return fail(MKV_ERR_HIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sd != cur)
+      return fail(MKV_ERR_ARG, "stream is on device %d but device %d is current; make the "
+                  "stream's device current", static_cast<int>(sd), cur);
+  }
+  if (cur < 0 || cur >= kMaxDevices) return fail(MKV_ERR_UNSUPPORTED, "device %d", cur);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[cur] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(MKV_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", cur,
+                  hipGetErrorString(e));
+    g_scratch_ptr[cur] = p;
+  }
+  *out = g_scratch_ptr[cur];
+  return MKV_OK;
+}
+
+}  // namespace
+
 // ------------------------------------------------------------------------ C ABI
 
 extern "C" const char* mkv_last_error(void) { return g_err; }
@@ -1044,7 +1095,11 @@ extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
   return launch_any<false>(dtype, g.uniform, sp, tiles, 1, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
+namespace {
+
+// The batched shift.  noalloc: the workspace is this device's `scratch` array and the
+// descriptor's workspace fields are ignored.
+int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   g_err[0] = '\0';
   if (d == nullptr) return fail(MKV_ERR_ARG, "NULL descriptor");
   const int eb = elem_bytes(d->dtype);
@@ -1068,7 +1123,17 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
   const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary);
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* ws_ptr = d->workspace;
-  const int64_t ws_bytes = d->workspace_bytes;
+  int64_t ws_bytes = d->workspace_bytes;
+  if (noalloc) {
+    if (need > MKV_NOALLOC_SCRATCH_BYTES)
+      return fail(MKV_ERR_UNSUPPORTED,
+                  "this shift needs %lld bytes of workspace, more than the %lld bytes of "
+                  "the no-allocation scratch buffer (use mkv_shift_spans with a workspace)",
+                  (long long)need, (long long)MKV_NOALLOC_SCRATCH_BYTES);
+    rc = scratch_of(st, &ws_ptr);
+    if (rc != MKV_OK) return rc;
+    ws_bytes = MKV_NOALLOC_SCRATCH_BYTES;
+  }
   if (ws_ptr == nullptr || ws_bytes < need)
     return fail(MKV_ERR_ARG, "workspace of %lld bytes needed (mkv_shift_workspace_size)",
                 (long long)need);
@@ -1131,4 +1196,14 @@ extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
   sp.rows_per_wave = g.rows_per_wave;
   sp.heads_magic = g.heads_magic;
   return launch_any<true>(d->dtype, g.uniform, sp, tiles, d->layers, st);
+}
+
+}  // namespace
+
+extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
+  return shift_spans(d, stream, false);
+}
+
+extern "C" int mkv_shift_spans_noalloc(const mkv_shift_desc_t* d, void* stream) {
+  return shift_spans(d, stream, true);
 }

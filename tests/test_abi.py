@@ -154,6 +154,24 @@ def test_batched_entry_point_argument_errors_need_no_gpu():
     assert b"k_scale" in lib.mkv_last_error()
 
 
+def test_noalloc_entry_point_refuses_shifts_beyond_its_scratch_without_a_gpu():
+    """The no-allocation entry point checks its size limit before any HIP call."""
+    lib = _lib.lib()
+    assert lib.mkv_shift_spans_noalloc(None, None) == _lib.MKV_ERR_ARG
+    d = _lib.ShiftDesc()
+    d.heads, d.head_size, d.rotary, d.dtype, d.layers = 8, 128, 128, _lib.MKV_BF16, 2
+    d.n_spans, d.spans, d.inv_freq = 1, 1 << 20, 1 << 21
+    for side in (d.src, d.dst):
+        side.k_base, side.v_base = 1 << 24, 1 << 25
+        side.mode, side.block_size, side.groups = _lib.MKV_ADDR_FLAT, 1, 1
+    d.total_tokens = _lib.MKV_NOALLOC_SCRATCH_BYTES // 32  # records alone fill the buffer
+    assert lib.mkv_shift_workspace_size(d.total_tokens, 1, 128) > _lib.MKV_NOALLOC_SCRATCH_BYTES
+    assert lib.mkv_shift_spans_noalloc(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
+    assert b"no-allocation scratch" in lib.mkv_last_error()
+    d.n_spans = 0  # an empty shift is a no-op, as for mkv_shift_spans
+    assert lib.mkv_shift_spans_noalloc(ctypes.byref(d), None) == _lib.MKV_OK
+
+
 def test_python_api_refuses_tensors_off_the_gpu():
     src = torch.zeros(4, 8, 256, dtype=torch.bfloat16)
     kv = torch.zeros(4, 8, 16, 256, dtype=torch.bfloat16)
