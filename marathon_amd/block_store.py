@@ -45,13 +45,13 @@ from __future__ import annotations
 
 import bisect
 import heapq
-from collections import OrderedDict
 from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
 from .shift_store import DEFAULT_STORE_TOKENS
+from .store_core import StoreCore, Window
 
 
 def _no_blocks() -> np.ndarray:
@@ -59,11 +59,13 @@ def _no_blocks() -> np.ndarray:
 
 
 @dataclass
-class _BlockEntry:
+class _BlockEntry(Window):
+    """A session's blocks; under the truncate policy the window ``[base, filled)`` (from
+    :class:`~marathon_amd.store_core.Window`) says what is held, under the interval
+    policy ``valid`` does."""
+
     table: np.ndarray = field(default_factory=_no_blocks)  # logical block -> pool id (-1: none)
     held: int = 0  # pool blocks this session owns
-    base: int = -1  # truncate policy: first position ever written (-1: nothing yet)
-    filled: int = 0  # truncate policy: [base, filled) holds valid KV
     valid: list = field(default_factory=list)  # interval policy: sorted disjoint [lo, hi)
     layers: set = field(default_factory=set)  # layers saved at least once
 
@@ -85,7 +87,7 @@ def _covered(ivs: list, lo: int, hi: int) -> bool:
     return i >= 0 and ivs[i][0] <= lo and hi <= ivs[i][1]
 
 
-class BlockShiftStore:
+class BlockShiftStore(StoreCore):
     """Session-keyed KV in ``block_size``-token blocks of a per-layer device pool."""
 
     def __init__(
@@ -96,7 +98,7 @@ class BlockShiftStore:
         block_size: int = 16,
         truncate: bool = True,
     ) -> None:
-        self.budget = int(budget_tokens)
+        super().__init__(budget_tokens)
         self.block_size = int(block_size)
         if self.block_size <= 0 or self.budget <= 0:
             raise ValueError("budget_tokens and block_size must be positive")
@@ -104,26 +106,51 @@ class BlockShiftStore:
         self.device = device
         self.allocate = allocate
         self.truncate = bool(truncate)
-        self._sessions: OrderedDict[str, _BlockEntry] = OrderedDict()  # oldest first
         self._free = list(range(self.pool_blocks))  # a heap: lowest id first
         self._pools: dict[str, torch.Tensor] = {}
         self._sigs: dict[str, tuple] = {}  # layer -> (row shape, dtype) of its pool
-        self.hits = 0
-        self.misses = 0
-        self.evictions = 0
-        self.refusals = 0
-        self.loaded_token_layers = 0
-        self.saved_token_layers = 0
 
-    # ----------------------------------------------------------------- internals
+    # --------------------------------------------------------------- store hooks
 
-    def _touch(self, session: str) -> _BlockEntry:
-        entry = self._sessions.get(session)
-        if entry is None:
-            entry = self._sessions[session] = _BlockEntry()
+    def _new_entry(self) -> _BlockEntry:
+        return _BlockEntry()
+
+    def _admits(self, entry: _BlockEntry, start: int, n: int) -> bool:
+        return start >= 0 and (not self.truncate or entry.leaves_no_hole(start))
+
+    def _make_room(self, session: str, entry: _BlockEntry, start: int, end: int) -> bool:
+        return self._ensure_blocks(session, entry, start, end)
+
+    def _commit(self, entry: _BlockEntry, start: int, end: int) -> None:
+        if self.truncate:
+            entry.extend(start, end)
+            # everything above the new top is gone, as in the flat window: free it
+            self._release(entry, -(-end // self.block_size), entry.table.size)
         else:
-            self._sessions.move_to_end(session)
-        return entry
+            _add_interval(entry.valid, start, end)
+
+    def _holds(self, entry: _BlockEntry, start: int, n: int) -> bool:
+        if n <= 0 or start < 0:
+            return False
+        if self.truncate:
+            return entry.contains(start, n)
+        return _covered(entry.valid, start, start + n)
+
+    def _has_layer(self, entry: _BlockEntry, layer: str) -> bool:
+        return layer in entry.layers
+
+    def _held_tokens(self, entry: _BlockEntry) -> int:
+        if self.truncate:
+            return entry.size
+        return sum(hi - lo for lo, hi in entry.valid)
+
+    def _forget(self, entry: _BlockEntry) -> None:
+        self._release(entry, 0, entry.table.size)
+
+    def _extra_stats(self) -> dict:
+        return {"pool_blocks": self.pool_blocks, "free_blocks": len(self._free)}
+
+    # ----------------------------------------------------------------- allocator
 
     @property
     def used(self) -> int:
@@ -158,59 +185,14 @@ class BlockShiftStore:
             missing = np.array([k for k in range(k0, k1) if entry.table[k] < 0], dtype=np.int64)
         else:
             missing = k0 + np.flatnonzero(entry.table[k0:k1] < 0)
-        while len(self._free) < missing.size:
-            victim = next((s for s in self._sessions if s != session), None)
-            if victim is None:
-                return False
-            self.drop(victim)
-            self.evictions += 1
+        if not self._evict_until(session, lambda: len(self._free) >= missing.size):
+            return False
         if missing.size:
             entry.table[missing] = [heapq.heappop(self._free) for _ in range(missing.size)]
         entry.held += int(missing.size)
         return True
 
     # -------------------------------------------------------------------- public
-
-    def reserve(self, session: str, dst_start: int, n: int) -> bool:
-        """Make room for ``[dst_start, dst_start + n)``; False (nothing stored) when the
-        span cannot fit the budget or, under the truncate policy, would leave a hole
-        above ``filled``.  Idempotent (shift_store.py:177-199)."""
-        need = dst_start + n
-        entry = self._touch(session)
-        first = entry.base < 0 if self.truncate else not entry.valid
-        hole = self.truncate and not first and dst_start > entry.filled
-        if need > self.budget or n <= 0 or dst_start < 0 or hole:
-            self.refusals += 1
-            return False
-        if not self._ensure_blocks(session, entry, dst_start, need):
-            self.refusals += 1
-            return False
-        if self.truncate:
-            if first:
-                entry.base = dst_start
-            entry.filled = need
-            # everything above the new top is gone, as in the flat window: free it
-            self._release(entry, -(-need // self.block_size), entry.table.size)
-        else:
-            _add_interval(entry.valid, dst_start, need)
-        return True
-
-    def _holds(self, entry: _BlockEntry | None, start: int, n: int) -> bool:
-        if entry is None or n <= 0 or start < 0:
-            return False
-        if self.truncate:
-            return entry.base >= 0 and start >= entry.base and start + n <= entry.filled
-        return _covered(entry.valid, start, start + n)
-
-    def covers(self, session: str, start: int, n: int) -> bool:
-        """Whether ``[start, start + n)`` is held for ``session`` (counts a hit/miss)."""
-        ok = self._holds(self._sessions.get(session), start, n)
-        if ok:
-            self.hits += 1
-            self._touch(session)
-        else:
-            self.misses += 1
-        return ok
 
     def pool(self, layer: str) -> torch.Tensor | None:
         """The layer's pool ``[pool_blocks, block_size, heads, 2D]`` (None before any save)."""
@@ -288,34 +270,6 @@ class BlockShiftStore:
         tab = torch.from_numpy(self._sessions[session].table.astype(np.int64))
         return tab[pos // self.block_size].to(device), (pos % self.block_size).to(device)
 
-    def lookup(self, session: str, layer: str, start: int, n: int) -> bool:
-        """:meth:`read`'s check and accounting without the gather: what a load calls once
-        per (load, layer) (vllm_shift_connector.py:506-513)."""
-        entry = self._sessions.get(session)
-        if not self._holds(entry, start, n) or layer not in entry.layers:
-            return False
-        self.loaded_token_layers += n
-        self._touch(session)
-        return True
-
-    def lookup_layers(self, session: str, layers, start: int, n: int):
-        """:meth:`lookup` of every layer in order, with the same accounting; returns the
-        first layer that misses, or None when all hit."""
-        entry = self._sessions.get(session)
-        if not self._holds(entry, start, n):
-            return next(iter(layers), None)
-        hit = 0
-        try:
-            for layer in layers:
-                if layer not in entry.layers:
-                    return layer
-                self.loaded_token_layers += n
-                hit += 1
-            return None
-        finally:
-            if hit:
-                self._touch(session)  # the LRU order one touch per layer would leave
-
     def read(self, session: str, layer: str, start: int, n: int) -> torch.Tensor | None:
         """``[n, heads, 2D]`` rows of ``[start, start + n)`` (a gathered copy), or None
         where any position is not held (shift_store.py:238-250)."""
@@ -324,28 +278,3 @@ class BlockShiftStore:
         p = self._pools[layer]
         blk, off = self._rows(session, start, n, p.device)
         return p[blk, off]
-
-    def drop(self, session: str) -> None:
-        entry = self._sessions.pop(session, None)
-        if entry is not None:
-            self._release(entry, 0, entry.table.size)
-
-    def stats(self) -> dict:
-        def held(e: _BlockEntry) -> int:
-            if self.truncate:
-                return max(e.filled - max(e.base, 0), 0)
-            return sum(hi - lo for lo, hi in e.valid)
-
-        return {
-            "budget_tokens": self.budget,
-            "used_tokens": self.used,
-            "pool_blocks": self.pool_blocks,
-            "free_blocks": len(self._free),
-            "sessions": {s: held(e) for s, e in self._sessions.items()},
-            "hits": self.hits,
-            "misses": self.misses,
-            "evictions": self.evictions,
-            "refusals": self.refusals,
-            "loaded_token_layers": self.loaded_token_layers,
-            "saved_token_layers": self.saved_token_layers,
-        }

@@ -306,3 +306,65 @@ def test_paged_planes_split_and_fused_layouts():
     assert paged_planes(hnd, 16)[0] == "hnd"
     with pytest.raises(ValueError, match="fused 4-D or a split 5-D"):
         paged_planes(torch.zeros(3, 6, 16, 4, 128), 16)
+
+
+# ------------------------------------------- the store's own formulations, pinned
+
+
+def test_slots_equal_brute_force_and_refuse_what_the_table_cannot_hold():
+    """``slots`` expands blocks into their slots and slices the positions; brute force
+    maps each position through the table one by one."""
+    import numpy as np
+
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        bs = int(rng.choice([1, 4, 16, 24]))
+        table = rng.permutation(64)[: int(rng.integers(1, 20))].tolist()
+        lo = int(rng.integers(0, len(table) * bs))
+        hi = int(rng.integers(lo, len(table) * bs + 1))
+        want = [table[p // bs] * bs + p % bs for p in range(lo, hi)]
+        assert slots(table, lo, hi, bs).tolist() == want
+    assert slots([3], 5, 5, 16).numel() == 0
+    with pytest.raises(IndexError):
+        slots([3, 4], 0, 33, 16)
+    with pytest.raises(ValueError):
+        slots([3, 4], -1, 8, 16)
+
+
+def test_slab_capacity_doubles_from_the_floor_and_stops_at_the_budget():
+    """Capacities a session's slabs take as it grows: the first fits the save in the
+    smallest slab * 2^k, later ones double the current capacity first."""
+    from marathon_amd.shift_store import _doubled
+
+    for floor in (1, 3, 256, 2048):
+        for want in (1, floor, floor + 1, 3 * floor, 4 * floor, 4 * floor + 1, 1000 * floor):
+            size = floor
+            while size < want:
+                size *= 2
+            assert _doubled(floor, want) == size
+    st = ShiftStore(budget_tokens=20000, device="cpu", allocate=False, slab=1000)
+    caps = []
+    for end in (10, 1000, 1001, 2500, 4001, 9000, 17000):
+        assert st.reserve("a", 0, end)
+        caps.append(st._sessions["a"].capacity)
+    assert caps == [1000, 1000, 2000, 4000, 8000, 16000, 20000]
+
+
+def test_growth_evicts_least_recently_used_others_until_it_fits():
+    """Three sessions fill the budget; touching one through ``covers`` (the scheduler)
+    or ``read`` (the worker) makes it the last to go when a fourth grows."""
+    for touch in ("covers", "read"):
+        st = ShiftStore(budget_tokens=8, device="cpu", slab=2)
+        for s in ("a", "b", "c"):
+            assert st.reserve(s, 0, 2)
+            st.write(s, "l0", 0, torch.zeros(2, 1, 2))
+        if touch == "covers":
+            assert st.covers("a", 0, 2)
+        else:
+            assert st.read("a", "l0", 0, 2) is not None
+        assert st.reserve("d", 0, 2) and st.evictions == 0  # 8 of 8 used
+        assert st.reserve("d", 2, 2)  # d grows 2 -> 4: evicts b (oldest untouched)
+        assert list(st._sessions) == ["c", "a", "d"] and st.evictions == 1
+        assert st.reserve("d", 4, 1)  # 4 -> 8: evicts c, then a
+        assert list(st._sessions) == ["d"] and st.evictions == 3
+        assert st.stats()["used_tokens"] == 8
