@@ -273,7 +273,7 @@ class ShiftLoader:
         self.verify_log: list = []  # one dict per (load, layer) checked
         self.block_size = int(block_size)
         self.inv_freq = inv_freq.detach().to(torch.float32).cpu()
-        self.k_scales = k_scales or {}
+        self.k_scales = k_scales if k_scales is not None else {}  # shared, may fill later
         self.timing = timing
         self._kv: dict[str, torch.Tensor] = {}
         self._planes: dict[str, tuple] = {}  # name -> (K, V or None), see paged_planes
@@ -283,6 +283,11 @@ class ShiftLoader:
         self.head_size: int | None = None
         self.last_plan: ShiftPlan | None = None
         self._sets = _CacheSets(self.block_size)
+
+    @property
+    def layer_names(self) -> list:
+        """The registered layers, in the order their caches were given."""
+        return list(self._kv)
 
     def register_kv_caches(self, kv_caches: dict) -> None:
         """Record the per-layer paged caches and their layout (:393-412): fused 4-D, as

@@ -231,6 +231,87 @@ class ScheduledKVEngine(RealKVEngine):
         self.declines = self.sched.declines
 
 
+class ConnectorKVEngine(RealKVEngine):
+    """Every decision and every copy through the connector object as vLLM drives it: one
+    ``MarathonShiftConnector`` per role, the scheduler's hooks fed vLLM-shaped requests
+    and scheduler outputs, the worker's hooks a forward context whose attention layers
+    hold the paged caches (stand-ins: tests/vllm_fakes.py).  Saves go through the
+    per-layer ``save_kv_layer`` hook and are flushed by ``wait_for_save``."""
+
+    def __init__(self, dev, store="blocks", device_slots=True, **kw):
+        from marathon_amd.vllm_connector import MarathonShiftConnector
+        from tests import vllm_fakes as F
+
+        super().__init__(dev, store=store, device_slots=True, **kw)
+        self.F = F
+        extra = {"store_layout": "block" if store == "blocks" else "flat",
+                 "store_tokens": 1 << 14 if store == "blocks" else 1 << 16,
+                 "store_device": str(dev)}
+        cfg = F.vllm_config(block_size=BS, extra=extra)
+        self.sched = MarathonShiftConnector(cfg, "scheduler")
+        self.worker = MarathonShiftConnector(cfg, "worker")
+        self.store = self.worker.store
+        self.fwd = F.forward_context(self.kv)
+        self.n_req = 0
+        self.loaded_tokens = 0
+
+    def _step(self, meta, ids, lo, hi, blocks):
+        """One forward pass: loads, the computed tokens' fresh KV, per-layer saves."""
+        w = self.worker
+        w.bind_connector_metadata(meta)
+        w.start_load_kv(self.fwd)
+        for ld in meta.loads:
+            sl = ScheduledKVEngine._paged(ld, ld.src_start + ld.delta)
+            st = self.store_shifts[ld.session]
+            self.shifts[sl] = st[ld.src_start:ld.src_start + ld.n] + int(ld.delta != 0)
+            self.loads += 1
+            self.loaded_tokens += ld.n
+        self._write_fresh(blocks, ids, lo, hi)
+        for name, cache in self.kv.items():
+            w.save_kv_layer(name, cache, None)
+        w.wait_for_save()
+        for sv in meta.saves:
+            sl = ScheduledKVEngine._paged(sv, sv.dst_start)
+            st = self.store_shifts.setdefault(sv.session, torch.zeros(1 << 16, dtype=torch.int32))
+            st[sv.dst_start:sv.dst_start + sv.n] = self.shifts[sl]
+        w.clear_connector_metadata()
+
+    def generate(self, ids, session, max_tokens, load=None, save=False):
+        F = self.F
+        rid = f"req{self.n_req}"
+        self.n_req += 1
+        blocks, hit = self._blocks_for(ids)
+        req = F.Request(rid, {"session": session, "load": load, "save": save}, len(ids))
+        self.sched.on_new_request(req)
+        ext, is_async = self.sched.get_num_new_matched_tokens(req, hit)
+        assert is_async is False
+        self.sched.update_state_after_alloc(req, None, ext)
+        computed = hit + ext
+        meta = self.sched.build_connector_meta(
+            F.step_output(new=[(rid, blocks, computed, len(ids) - computed)]))
+        assert len(meta.loads) == int(ext > 0)
+        self._step(meta, ids, computed, len(ids), blocks)
+        torch.cuda.synchronize(self.dev)
+        self._verify(blocks, ids)
+        cur_ids = list(ids)
+        for _ in range(max_tokens):
+            cur = len(cur_ids)
+            new = None
+            if cur // BS >= len(blocks):
+                new = [self.next_block]
+                blocks.append(self.next_block)
+                self.next_block += 1
+            meta = self.sched.build_connector_meta(F.step_output(cached=[(rid, new, cur, 1)]))
+            assert not meta.loads
+            cur_ids.append(1)
+            self._step(meta, cur_ids, cur, cur + 1, blocks)
+        assert self.sched.request_finished(req, blocks) == (False, None)
+        for k in range(len(ids) // BS):
+            self.prefix.setdefault(tuple(ids[: (k + 1) * BS]), blocks[k])
+        torch.cuda.synchronize(self.dev)
+        self.declines = self.sched._sched.declines
+
+
 def _prompt(messages):
     pieces = [list(f"{m['role']}: {m['content']}\n".encode()) for m in messages]
     return [i for p in pieces for i in p] + [10], pieces
@@ -248,10 +329,12 @@ def _phases(load, n_prompt):
 @pytest.mark.parametrize("store,device_slots,engine", [
     ("flat", False, RealKVEngine), ("flat", True, RealKVEngine),
     ("blocks", False, RealKVEngine), ("blocks", True, RealKVEngine),
-    ("flat", False, ScheduledKVEngine), ("blocks", True, ScheduledKVEngine)])
+    ("flat", False, ScheduledKVEngine), ("blocks", True, ScheduledKVEngine),
+    ("blocks", True, ConnectorKVEngine), ("flat", True, ConnectorKVEngine)])
 def test_front_edits_through_the_real_kernels(gpu, store, device_slots, engine):
     """``ScheduledKVEngine`` takes every decision through the connector's scheduler
-    half; the others call the planners directly."""
+    half, ``ConnectorKVEngine`` every decision and copy through the connector object's
+    hooks; the others call the planners directly."""
     eng = engine(gpu, store=store, device_slots=device_slots)
     messages, keep_last, turns = [], 3, 9
     prompt_pieces = None  # pieces of the previous request's prompt: what the store holds
@@ -284,6 +367,17 @@ def test_front_edits_through_the_real_kernels(gpu, store, device_slots, engine):
         messages.append({"role": "assistant", "content": f"ok {t}"})
     assert eng.loads >= turns - keep_last - 1, (eng.loads, eng.declines)
     assert int(eng.shifts.max()) >= 2  # some KV was re-rotated more than once
+    if engine is ConnectorKVEngine:
+        from marathon_amd.vllm_connector import merged_stats
+
+        sched, worker = eng.sched.store.stats(), eng.worker.store.stats()
+        # the scheduler's mirror and the worker's store took the same decisions
+        assert sched["sessions"] == worker["sessions"]
+        assert sched["hits"] == eng.loads  # one coverage check per load served
+        assert worker["loaded_token_layers"] == eng.loaded_tokens * LAYERS
+        merged = merged_stats([eng.sched.store, eng.worker.store])
+        assert merged["sessions"] == worker["sessions"]
+        assert merged["saved_token_layers"] == worker["saved_token_layers"]
 
 
 def test_saver_matches_a_torch_gather(gpu):
