@@ -80,6 +80,9 @@ extern "C" {
 /* Limits of the batched entry point. */
 #define MKV_MAX_SPANS 4096
 #define MKV_MAX_HEAD_SIZE 512
+#define MKV_DIRECT_MAX_SPANS 63 /* spans of a direct (single-launch) shift */
+#define MKV_SMALL_MAX_SPANS 8   /* spans of a small shift (mkv_shift_spans_small) */
+#define MKV_SMALL_MAX_INDEX 64  /* index entries per side of a small shift */
 
 /*
  * One reused span: n_tokens consecutive tokens whose K moves by `delta` positions.
@@ -145,7 +148,21 @@ typedef struct mkv_side {
  *   error_flags  : device int32 [1] or NULL.
  *   workspace    : device, >= mkv_shift_workspace_size(total_tokens, n_spans, rotary)
  *                  bytes, 16-byte aligned; overwritten by every call, so calls that
- *                  overlap on one workspace race.
+ *                  overlap on one workspace race.  Not needed on the direct path.
+ *   span_starts, span_tables : optional, together: the direct path, one launch and no
+ *                  workspace.  span_starts is device int64 [n_spans + 1], the exclusive
+ *                  prefix sum of the spans' max(n_tokens, 0) (span_starts[0] == 0,
+ *                  span_starts[n_spans] <= total_tokens); span_tables is device fp32
+ *                  [n_spans][2][rotary], 16-byte aligned: for span s, the rotary cos
+ *                  values by element, then the rotary signed sines by element, in the
+ *                  header's notation cos(a[i mod rotary/2]) and sgn[i], each rounded to
+ *                  fp32 (the values the plan pass would compute).  Taken when
+ *                  n_spans <= MKV_DIRECT_MAX_SPANS, both sides' block sizes are powers
+ *                  of two, and heads is a multiple of the rows one wave covers
+ *                  (64 / (head_size * element bytes / 16)); otherwise
+ *                  ignored, and the two-launch path with its workspace runs.  A prefix
+ *                  that disagrees with the spans raises MKV_FLAG_SPAN; its tokens are
+ *                  bounds-checked like any other.
  */
 typedef struct mkv_shift_desc {
   const mkv_span_t* spans;
@@ -163,6 +180,8 @@ typedef struct mkv_shift_desc {
   int32_t dtype;
   mkv_side_t src;
   mkv_side_t dst;
+  const int64_t* span_starts;
+  const float* span_tables;
 } mkv_shift_desc_t;
 
 /*
@@ -207,6 +226,25 @@ int mkv_scatter_shifted(const void* src, int64_t src_token_stride, int64_t src_h
 int mkv_shift_spans(const mkv_shift_desc_t* desc, void* stream);
 
 /*
+ * A small batched shift -- a decode step's saves, a short load -- as one launch that
+ * carries its span table, token prefix and index windows in the launch's own kernel
+ * arguments: nothing is copied to the device first and no workspace is used.  Same
+ * semantics, checks and results as mkv_shift_spans, with these differences:
+ *   - desc->spans and desc->src.index / desc->dst.index are HOST pointers, read during
+ *     the call (the caller may reuse them as soon as it returns);
+ *   - n_spans <= MKV_SMALL_MAX_SPANS and each side's index_len <= MKV_SMALL_MAX_INDEX;
+ *     both sides' block sizes powers of two; heads a multiple of the rows one wave covers
+ *     (64 / (head_size * element bytes / 16)); otherwise MKV_ERR_UNSUPPORTED;
+ *   - the token prefix is computed here: a span with n_tokens < 0, or spans that hold
+ *     more than total_tokens tokens, are MKV_ERR_ARG;
+ *   - the rotation tables are computed in the kernel from inv_freq as the plan pass
+ *     computes them; desc->workspace, span_starts and span_tables are ignored.
+ * Replaces the reference connector's per-layer, per-save launches for a decode step
+ * (src/marathon/vllm_shift_connector.py:539-553) and short loads (:505-518).
+ */
+int mkv_shift_spans_small(const mkv_shift_desc_t* desc, void* stream);
+
+/*
  * mkv_shift_spans without a workspace argument: the same shift, the same checks and the
  * same results, with its workspace in a library-owned device buffer of
  * MKV_NOALLOC_SCRATCH_BYTES on each GPU (held from the library's first use on that GPU
@@ -232,7 +270,7 @@ const char* mkv_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. */
 int32_t mkv_abi_version(void);
-#define MKV_ABI_VERSION ((2 << 16) | 1)
+#define MKV_ABI_VERSION ((3 << 16) | 1)
 
 #ifdef __cplusplus
 }

@@ -42,7 +42,10 @@ MKV_ADDR_TABLE = 2
 
 MKV_MAX_SPANS = 4096
 MKV_MAX_HEAD_SIZE = 512
-MKV_ABI_VERSION = (2 << 16) | 1
+MKV_DIRECT_MAX_SPANS = 63
+MKV_SMALL_MAX_SPANS = 8
+MKV_SMALL_MAX_INDEX = 64
+MKV_ABI_VERSION = (3 << 16) | 1
 MKV_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 ERROR_NAMES = {
@@ -58,6 +61,7 @@ EXPORTED = (
     "mkv_scatter_shifted",
     "mkv_shift_spans",
     "mkv_shift_spans_noalloc",
+    "mkv_shift_spans_small",
     "mkv_shift_workspace_size",
     "mkv_last_error",
     "mkv_abi_version",
@@ -116,7 +120,7 @@ class Side(ctypes.Structure):
 
 
 class ShiftDesc(ctypes.Structure):
-    """mkv_shift_desc_t (256 bytes)."""
+    """mkv_shift_desc_t (272 bytes)."""
 
     _fields_ = [
         ("spans", ctypes.c_void_p),
@@ -134,10 +138,12 @@ class ShiftDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("src", Side),
         ("dst", Side),
+        ("span_starts", ctypes.c_void_p),
+        ("span_tables", ctypes.c_void_p),
     ]
 
 
-assert ctypes.sizeof(Side) == 88 and ctypes.sizeof(ShiftDesc) == 256
+assert ctypes.sizeof(Side) == 88 and ctypes.sizeof(ShiftDesc) == 272
 
 
 class KVShiftError(RuntimeError):
@@ -158,7 +164,7 @@ def _bind(cdll: ctypes.CDLL) -> ctypes.CDLL:
     f.restype = ctypes.c_int
     f.argtypes = [vp, i64, i64, vp, i64, i64, i64, i64, vp, i64, i32, i32, i32, i32, vp, vp,
                   i32, vp, vp, vp]
-    for name in ("mkv_shift_spans", "mkv_shift_spans_noalloc"):
+    for name in ("mkv_shift_spans", "mkv_shift_spans_noalloc", "mkv_shift_spans_small"):
         f = getattr(cdll, name)
         f.restype = ctypes.c_int
         f.argtypes = [ctypes.POINTER(ShiftDesc), vp]

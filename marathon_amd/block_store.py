@@ -109,6 +109,8 @@ class BlockShiftStore(StoreCore):
         self._free = list(range(self.pool_blocks))  # a heap: lowest id first
         self._pools: dict[str, torch.Tensor] = {}
         self._sigs: dict[str, tuple] = {}  # layer -> (row shape, dtype) of its pool
+        self._pool_lists: dict[tuple, tuple] = {}  # layers -> (pools existing, their list)
+        self._sig_ok: dict[tuple, tuple] = {}  # layers -> the row signature all pools have
 
     # --------------------------------------------------------------- store hooks
 
@@ -198,6 +200,15 @@ class BlockShiftStore(StoreCore):
         """The layer's pool ``[pool_blocks, block_size, heads, 2D]`` (None before any save)."""
         return self._pools.get(layer)
 
+    def pools(self, layers) -> list:
+        """:meth:`pool` of each layer, as one list reused while no pool changes (a step's
+        loader and saver ask for the same layers every step)."""
+        key = tuple(layers)
+        got = self._pool_lists.get(key)
+        if got is None or got[0] != len(self._pools):
+            got = self._pool_lists[key] = (len(self._pools), [self._pools.get(n) for n in key])
+        return got[1]
+
     def _pool_for(self, layer: str, row_shape, dtype, device) -> torch.Tensor:
         sig = (tuple(row_shape), dtype)
         p = self._pools.get(layer)
@@ -240,10 +251,18 @@ class BlockShiftStore(StoreCore):
         if not self._positions_ok(entry, dst_start, n):
             return None
         sig = (tuple(row_shape), dtype)
-        pools, sigs = self._pools, self._sigs
-        out = [pools[layer] if sigs.get(layer) == sig else
-               self._pool_for(layer, row_shape, dtype, device) for layer in layers]
-        entry.layers.update(layers)
+        key = tuple(layers)
+        hit = self._pool_lists.get(key)
+        if hit is not None and hit[0] == len(self._pools) and self._sig_ok.get(key) == sig:
+            out = hit[1]  # the steady state: every pool exists with these rows
+        else:
+            pools, sigs = self._pools, self._sigs
+            out = [pools[layer] if sigs.get(layer) == sig else
+                   self._pool_for(layer, row_shape, dtype, device) for layer in layers]
+            self._pool_lists[key] = (len(self._pools), out)
+            self._sig_ok[key] = sig
+        if not entry.layers.issuperset(key):
+            entry.layers.update(key)
         self.saved_token_layers += n * len(out)
         return out
 

@@ -35,7 +35,7 @@ import torch
 from . import _lib
 from .block_store import BlockShiftStore
 from .shift_store import ShiftStore, slots as host_slots
-from .spans import CacheSet, ShiftPlan
+from .spans import CacheSet, ShiftPlan, SmallShifts
 
 logger = logging.getLogger("marathon_amd.shift")
 
@@ -143,52 +143,105 @@ class _CacheSets:
     """CacheSets by role, rebuilt only when the tensors they describe change.
 
     A CacheSet validates every tensor and reads every base address once; a step that
-    reuses the same caches should not pay that again.  The key is the tensors' ids:
-    the cached set keeps its tensors alive, so an id cannot be reused while cached.
+    reuses the same caches should not pay that again.  Rows given as the very list
+    objects of the cached set match at once; otherwise the tensors' ids are compared
+    (the cached set keeps its tensors alive, so an id cannot be reused while cached).
     """
 
     def __init__(self, block_size: int) -> None:
         self.block_size = block_size
         self._sets: dict[str, tuple] = {}
 
+    @staticmethod
+    def _ids(rows) -> tuple | None:
+        return None if rows is None else tuple(tuple(id(t) for t in row) for row in rows)
+
     def get(self, role: str, caches: list, layout: str, block_size: int | None = None,
             v_caches: list | None = None) -> CacheSet:
-        key = (tuple(tuple(id(t) for t in row) for row in caches),
-               None if v_caches is None else tuple(tuple(id(t) for t in row) for row in v_caches))
         hit = self._sets.get(role)
-        if hit is None or hit[0] != key:
-            bs = self.block_size if block_size is None else block_size
-            hit = self._sets[role] = (key, CacheSet(
-                [list(r) for r in caches], layout, bs,
-                v_caches=None if v_caches is None else [list(r) for r in v_caches]))
-        return hit[1]
+        if hit is not None:
+            rows, v_rows, _, cs = hit
+            same = len(rows) == len(caches) and all(a is b for a, b in zip(rows, caches)) and (
+                v_caches is None if v_rows is None else
+                v_caches is not None and len(v_rows) == len(v_caches)
+                and all(a is b for a, b in zip(v_rows, v_caches)))
+            if same or hit[2] == (self._ids(caches), self._ids(v_caches)):
+                if not same:
+                    self._sets[role] = (list(caches), None if v_caches is None else
+                                        list(v_caches), hit[2], cs)
+                return cs
+        bs = self.block_size if block_size is None else block_size
+        cs = CacheSet([list(r) for r in caches], layout, bs,
+                      v_caches=None if v_caches is None else [list(r) for r in v_caches])
+        self._sets[role] = (list(caches), None if v_caches is None else list(v_caches),
+                            (self._ids(caches), self._ids(v_caches)), cs)
+        return cs
+
+
+class _SmallRunners:
+    """One :class:`~marathon_amd.spans.SmallShifts` per (source set, destination set,
+    modes, K scales), reused across steps while those stay the same objects."""
+
+    def __init__(self) -> None:
+        self._runners: dict[tuple, tuple] = {}
+
+    def get(self, src: CacheSet, dst: CacheSet, src_mode: str, dst_mode: str, inv_freq,
+            k_scale=None) -> SmallShifts:
+        scales = None if k_scale is None else tuple(k_scale.tolist())
+        key = (id(src), id(dst), src_mode, dst_mode, scales)
+        hit = self._runners.get(key)
+        if hit is None or hit[0] is not src or hit[1] is not dst:
+            if len(self._runners) >= 16:  # caches or stores replaced many times over
+                self._runners.clear()
+            hit = self._runners[key] = (src, dst, SmallShifts(
+                src, dst, inv_freq=inv_freq, src_mode=src_mode, dst_mode=dst_mode,
+                k_scale=k_scale))
+        return hit[2]
+
+
+def _host(index) -> np.ndarray | None:
+    return None if index is None else index.numpy()
+
+
+def _int32_table(t) -> np.ndarray:
+    if isinstance(t, np.ndarray) and t.dtype == np.int32:
+        return t.reshape(-1)
+    if isinstance(t, torch.Tensor):
+        return t.detach().to("cpu", torch.int32).numpy().reshape(-1)
+    return np.asarray(t, dtype=np.int32).reshape(-1)
+
+
+def table_window(table: np.ndarray, pos: int, n: int, block_size: int):
+    """The blocks of ``table`` that positions ``[pos, pos + n)`` touch, and ``pos``
+    relative to the first of them: only those entries need to reach the device."""
+    k0 = pos // block_size
+    k1 = -(-(pos + n) // block_size)
+    if pos < 0 or k1 > table.size:
+        raise ValueError(f"positions [{pos}, {pos + n}) exceed a block table of "
+                         f"{table.size} blocks")
+    return table[k0:k1], pos - k0 * block_size
 
 
 def paged_index(items: list, block_size: int):
     """Address the paged side of a batch of loads or saves: ``(mode, index, rows)``.
 
-    When no item carries host slots, the block tables are concatenated (int32) and each
-    item gets ``(pos, offset)``: position ``pos + i`` resolves through
-    ``table[offset + (pos + i) // block_size]`` on the device.  Otherwise the slots are
-    concatenated (int64; ``from_blocks`` items are expanded on the host) and each item
-    gets ``(0, offset)`` into them.
+    When no item carries host slots, each item's window of its block table (the blocks
+    its positions touch) is concatenated (int32) and the item gets ``(pos, offset)``:
+    position ``pos + i`` resolves through ``table[offset + (pos + i) // block_size]`` on
+    the device.  Otherwise the slots are concatenated (int64; ``from_blocks`` items are
+    expanded on the host) and each item gets ``(0, offset)`` into them.
     """
     if all(it.slots is None for it in items):
         tabs, rows, off = [], [], 0
-        seen: dict[int, tuple] = {}  # items of one request share its block table
+        tables: dict[int, np.ndarray] = {}  # items of one request share its block table
         for it in items:
-            hit = seen.get(id(it.block_ids))
-            if hit is None:
-                t = it.block_ids
-                t = t.cpu().numpy() if isinstance(t, torch.Tensor) else t
-                t = np.asarray(t, dtype=np.int32).reshape(-1)
-                hit = seen[id(it.block_ids)] = (off, t.size)
-                tabs.append(t)
-                off += t.size
-            if it.paged_pos < 0 or it.paged_pos + it.n > hit[1] * block_size:
-                raise ValueError(f"positions [{it.paged_pos}, {it.paged_pos + it.n}) exceed "
-                                 f"a block table of {hit[1]} blocks")
-            rows.append((it.paged_pos, hit[0]))
+            t = tables.get(id(it.block_ids))
+            if t is None:
+                t = tables[id(it.block_ids)] = _int32_table(it.block_ids)
+            win, pos = table_window(t, it.paged_pos, it.n, block_size)
+            tabs.append(win)
+            rows.append((pos, off))
+            off += win.size
         return "table", torch.from_numpy(np.concatenate(tabs)), rows
     parts, rows, off = [], [], 0
     for it in items:
@@ -200,6 +253,18 @@ def paged_index(items: list, block_size: int):
         rows.append((0, off))
         off += int(sl.numel())
     return "slots", torch.cat(parts), rows
+
+
+def _store_windows(store, items, start_of) -> tuple:
+    """The block store's side of a batch: each item's window of its session's block
+    table, concatenated, and per item ``(pos, offset)`` (see :func:`table_window`)."""
+    tabs, rows, off = [], [], 0
+    for it in items:
+        win, pos = table_window(store.table(it.session), start_of(it), it.n, store.block_size)
+        tabs.append(win)
+        rows.append((pos, off))
+        off += win.size
+    return torch.from_numpy(np.concatenate(tabs)), rows
 
 
 def detect_hnd(shape, block_size: int) -> bool:
@@ -281,8 +346,9 @@ class ShiftLoader:
         self.hnd: bool | None = None
         self.split = False
         self.head_size: int | None = None
-        self.last_plan: ShiftPlan | None = None
+        self.last_plan: ShiftPlan | SmallShifts | None = None
         self._sets = _CacheSets(self.block_size)
+        self._small = _SmallRunners()
 
     @property
     def layer_names(self) -> list:
@@ -301,6 +367,9 @@ class ShiftLoader:
         self.hnd = layout == "hnd"
         self.split = v is not None
         self.head_size = k.shape[3] if self.split else k.shape[3] // 2
+        planes = list(self._planes.values())
+        self._paged = CacheSet([[k for k, _ in planes]], layout, self.block_size,
+                               v_caches=[[v for _, v in planes]] if self.split else None)
         one = next(iter(self._kv.values()))
         if one.is_cuda:
             _lib.lib()  # the kernels are compiled ahead of time: only load the library
@@ -337,19 +406,14 @@ class ShiftLoader:
         dst_mode, dst_index, dst_rows = paged_index(taken, self.block_size)
         rows = []
         if blocky:
-            # one pool per layer; each session's block table is the source index
-            tab_off, tabs, off = {}, [], 0
-            for sess in groups:
-                t = self.store.table(sess)
-                tab_off[sess] = off
-                tabs.append(t)
-                off += t.size
-            src = self._sets.get("store", [[self.store.pool(name) for name in names]], "nhd",
+            # one pool per layer; each load's window of its session's block table is
+            # the source index
+            src = self._sets.get("store", [self.store.pools(names)], "nhd",
                                  self.store.block_size)
-            src_mode, src_index = "table", torch.from_numpy(np.concatenate(tabs))
-            for load, (dpos, didx) in zip(taken, dst_rows):
-                rows.append((load.src_start, dpos, tab_off[load.session], didx, load.n,
-                             int(load.delta), 0, 0))
+            src_mode = "table"
+            src_index, src_rows = _store_windows(self.store, taken, lambda ld: ld.src_start)
+            for load, (spos, sidx), (dpos, didx) in zip(taken, src_rows, dst_rows):
+                rows.append((spos, dpos, sidx, didx, load.n, int(load.delta), 0, 0))
         else:
             src = self._sets.get(
                 "store", [[self.store.buffer(sess, name) for name in names] for sess in groups],
@@ -358,34 +422,37 @@ class ShiftLoader:
             for load, (dpos, didx) in zip(taken, dst_rows):
                 rows.append((load.src_start, dpos, 0, didx, load.n, int(load.delta),
                              groups[load.session], 0))
-        planes = list(self._planes.values())
-        dst = self._sets.get("paged", [[k for k, _ in planes]], self.layout,
-                             v_caches=[[v for _, v in planes]] if self.split else None)
+        dst = self._paged
         k_scale = None
         if dst.first.dtype == torch.float8_e4m3fn:
             k_scale = torch.tensor([float(self.k_scales.get(name, 1.0)) for name in names])
-        plan = ShiftPlan(
-            np.array(rows, dtype=_lib.SPAN_DTYPE),
-            src,
-            dst,
-            inv_freq=self.inv_freq,
-            src_mode=src_mode,
-            src_index=src_index,
-            dst_mode=dst_mode,
-            dst_index=dst_index,
-            k_scale=k_scale,
-        )
+        tokens = sum(load.n for load in taken)
         t0 = 0.0
         if self.timing:
             torch.cuda.synchronize(dst.first.device)
             t0 = time.perf_counter()
-        plan.launch()
+        small = self._small.get(src, dst, src_mode, dst_mode, self.inv_freq, k_scale)
+        if small.fits(len(rows), tokens):  # a short load: no plan to build
+            small.run(rows, _host(src_index), _host(dst_index))
+            plan = small
+        else:
+            plan = ShiftPlan(
+                np.array(rows, dtype=_lib.SPAN_DTYPE),
+                src,
+                dst,
+                inv_freq=self.inv_freq,
+                src_mode=src_mode,
+                src_index=src_index,
+                dst_mode=dst_mode,
+                dst_index=dst_index,
+                k_scale=k_scale,
+            )
+            plan.launch()
         self.last_plan = plan
         if self.verify:
             for load in taken:
                 for name in names:
                     self._verify(name, load, k_scale, names.index(name))
-        tokens = sum(load.n for load in taken)
         if self.timing:
             torch.cuda.synchronize(dst.first.device)
             ms = (time.perf_counter() - t0) * 1e3
@@ -492,6 +559,7 @@ class ShiftScheduler:
         self._blocks: dict[str, list] = {}
         self._need_load: set[str] = set()
         self._step_tables: dict[str, np.ndarray] = {}
+        self._np_tables: dict[str, np.ndarray] = {}
         self.declines: list[str] = []
 
     def on_new_request(self, rid: str, params: dict | None) -> None:
@@ -526,11 +594,19 @@ class ShiftScheduler:
             self._need_load.add(rid)
 
     def _table_of(self, rid: str):
-        """The request's block table as of this step, one object per request per step:
-        a step's load and saves of one request then share one device table."""
+        """The request's block table as of this step (int32), one object per request per
+        step: a step's load and saves of one request then share it.  Kept as a numpy
+        array that grows with the request, so a decode step converts no list."""
         tab = self._step_tables.get(rid)
         if tab is None:
-            tab = self._step_tables[rid] = np.asarray(self._blocks[rid], np.int32)
+            blocks = self._blocks[rid]
+            have = self._np_tables.get(rid)
+            if have is None or have.size > len(blocks):
+                have = np.asarray(blocks, np.int32)
+            elif have.size < len(blocks):
+                have = np.concatenate((have, np.asarray(blocks[have.size:], np.int32)))
+            self._np_tables[rid] = have
+            tab = self._step_tables[rid] = have
         return tab
 
     def _load(self, rid: str, lo: int, hi: int, delta: int) -> Load:
@@ -571,6 +647,7 @@ class ShiftScheduler:
         self._step_tables = {}
         for rid, block_ids, computed, scheduled in new_reqs:
             self._blocks[rid] = list(block_ids)
+            self._np_tables.pop(rid, None)  # a request scheduled anew gets a new table
             if rid in self._need_load:
                 lo, hi, delta = self._plans[rid]
                 meta.loads.append(self._load(rid, lo, hi, delta))
@@ -591,6 +668,7 @@ class ShiftScheduler:
 
     def _forget(self, rid: str) -> None:
         self._blocks.pop(rid, None)
+        self._np_tables.pop(rid, None)
         self._params.pop(rid, None)
         self._plans.pop(rid, None)
         self._need_load.discard(rid)
@@ -617,24 +695,31 @@ class ShiftSaver:
         self.last_plan: ShiftPlan | None = None
         self._sets = _CacheSets(self.block_size)
         self._pending: list = []  # deferred: (layer name, paged cache, the step's saves)
-        self._plane_memo: dict[int, tuple] = {}  # id(cache) -> (cache, layout, K, V)
+        self._geo: dict[tuple, tuple] = {}  # the caches of a step -> their geometry
+        self._small = _SmallRunners()
 
-    def _planes(self, t: torch.Tensor):
-        hit = self._plane_memo.get(id(t))
-        if hit is None or hit[0] is not t:
-            if len(self._plane_memo) > 4096:  # caches replaced many times over
-                self._plane_memo.clear()
-            hit = self._plane_memo[id(t)] = (t, *paged_planes(t, self.block_size))
-        return hit[1:]
+    def _geometry(self, caches: list) -> tuple:
+        """``(row_shape, dtype, device, paged CacheSet)`` of a step's paged caches, worked
+        out once per distinct tuple of cache tensors (vLLM passes the same ones every
+        step)."""
+        key = tuple(caches)
+        hit = self._geo.get(key)
+        if hit is None:
+            planes = [paged_planes(t, self.block_size) for t in caches]
+            layout, first, v_first = planes[0]
+            split = v_first is not None
+            # the store holds fused rows [heads, 2D] whichever way the cache keeps them
+            row_shape = (first.shape[1] if layout == "hnd" else first.shape[2],
+                         first.shape[3] * (2 if split else 1))
+            paged = CacheSet([[k for _, k, _ in planes]], layout, self.block_size,
+                             v_caches=[[v for _, _, v in planes]] if split else None)
+            if len(self._geo) >= 64:  # caches replaced many times over
+                self._geo.clear()
+            hit = self._geo[key] = (row_shape, first.dtype, first.device, paged)
+        return hit
 
     def _plan(self, names: list, caches: list, saves: list) -> int:
-        planes = [self._planes(t) for t in caches]
-        layout, first, v_first = planes[0]
-        hnd = layout == "hnd"
-        split = v_first is not None
-        # the store holds fused rows [heads, 2D] whichever way the paged cache keeps them
-        row_shape = (first.shape[1] if hnd else first.shape[2],
-                     first.shape[3] * (2 if split else 1))
+        row_shape, dtype, device, paged = self._geometry(caches)
         blocky = isinstance(self.store, BlockShiftStore)
         groups: dict[str, int] = {}
         bufs: list[list] = []
@@ -647,7 +732,7 @@ class ShiftSaver:
             if not self.store.reserve(save.session, save.dst_start, n):
                 continue
             targets = self.store.write_targets(save.session, names, save.dst_start, n,
-                                               row_shape, first.dtype, first.device)
+                                               row_shape, dtype, device)
             if targets is None:
                 continue
             g = groups.get(save.session)
@@ -665,26 +750,26 @@ class ShiftSaver:
         src_mode, src_index, src_rows = paged_index(taken, self.block_size)
         rows = []
         if blocky:
-            tab_off, tabs, off = {}, [], 0
-            for sess in groups:
-                t = self.store.table(sess)
-                tab_off[sess] = off
-                tabs.append(t)
-                off += t.size
-            dst = self._sets.get("store", [[self.store.pool(name) for name in names]], "nhd",
+            dst = self._sets.get("store", [self.store.pools(names)], "nhd",
                                  self.store.block_size)
-            dst_mode, dst_index = "table", torch.from_numpy(np.concatenate(tabs))
-            for sv, (spos, sidx) in zip(taken, src_rows):
-                rows.append((spos, int(sv.dst_start), sidx, tab_off[sv.session], sv.n, 0, 0, 0))
+            dst_mode = "table"
+            dst_index, dst_rows = _store_windows(self.store, taken, lambda sv: sv.dst_start)
+            for sv, (spos, sidx), (dpos, didx) in zip(taken, src_rows, dst_rows):
+                rows.append((spos, dpos, sidx, didx, sv.n, 0, 0, 0))
         else:
             dst = self._sets.get("store", bufs, "flat")
             dst_mode, dst_index = "flat", None
             for sv, (spos, sidx) in zip(taken, src_rows):
                 rows.append((spos, int(sv.dst_start), sidx, 0, sv.n, 0, 0, groups[sv.session]))
+        tokens = sum(sv.n for sv in taken)
+        small = self._small.get(paged, dst, src_mode, dst_mode, None)
+        if small.fits(len(rows), tokens):  # a decode step: no plan to build
+            small.run(rows, _host(src_index), _host(dst_index))
+            self.last_plan = small
+            return tokens * len(names)
         plan = ShiftPlan(
             np.array(rows, dtype=_lib.SPAN_DTYPE),
-            self._sets.get("paged", [[k for _, k, _ in planes]], layout,
-                           v_caches=[[v for _, _, v in planes]] if split else None),
+            paged,
             dst,
             inv_freq=None,
             src_mode=src_mode,
@@ -694,7 +779,7 @@ class ShiftSaver:
         )
         plan.launch()
         self.last_plan = plan
-        return sum(sv.n for sv in taken) * len(names)
+        return tokens * len(names)
 
     def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, saves: list) -> int:
         """One layer, every save of the step (the reference's per-layer hook).

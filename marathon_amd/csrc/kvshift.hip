@@ -196,9 +196,14 @@ struct ShiftParams {
   const float* sgn;
   int64_t src_tstride;  // BYTES
   DevSide dst;          // slot -> offset (single span)
-  // batched: records, per-span tables, base-address tables
+  // batched: records (or, direct, the span table and its token prefix), per-span
+  // tables, base-address tables
   const TokRec* recs;
+  const mkv_span_t* spans;
+  const int64_t* starts;  // direct: [n_spans + 1] exclusive prefix of n_tokens
+  DevSide src;            // direct: source addressing (dst above is the destination's)
   const float* tables;
+  const float* inv_freq;  // small: the tables are computed from it in the kernel
   const uint64_t* src_k_base;
   const uint64_t* src_v_base;
   const uint64_t* dst_k_base;
@@ -217,6 +222,22 @@ struct ShiftParams {
   int32_t rows_per_wave;
   uint32_t heads_magic;  // ceil(2^32 / heads): r / heads == umulhi(r, magic), r < 2^16
   int32_t rotate;        // single span: tables present
+  int32_t n_spans;       // direct
+};
+
+// A small shift's tables, carried in the launch's kernel arguments (no device copy):
+// the span table, its token prefix and each side's index window (int64, block ids or
+// slots).  ~1.5 KB of the 4 KB kernel-argument limit.
+struct SmallPack {
+  mkv_span_t spans[MKV_SMALL_MAX_SPANS];
+  int64_t starts[MKV_SMALL_MAX_SPANS + 1];
+  int64_t src_index[MKV_SMALL_MAX_INDEX];
+  int64_t dst_index[MKV_SMALL_MAX_INDEX];
+};
+
+struct SmallParams {
+  ShiftParams p;
+  SmallPack q;
 };
 
 // ------------------------------------------------------------------ small helpers
@@ -434,6 +455,65 @@ __device__ __forceinline__ bool resolve(const DevSide& sd, int64_t cap, int64_t 
   return true;
 }
 
+// resolve() for the direct path: block sizes that are powers of two (shifts only, no
+// 64-bit division) and wave-uniform indices (scalar loads).
+// `small`: the index is the launch's own int64 window, not the side's device array.
+__device__ __forceinline__ bool resolve_direct(const DevSide& sd, const int64_t* small,
+                                               int64_t cap, int64_t pos0, int64_t index0,
+                                               int64_t i, int64_t& off_bytes) {
+  const int sh = sd.bs_shift;
+  int64_t blk, off;
+  if (sd.mode == MKV_ADDR_TABLE) {
+    const int64_t pos = pos0 + i;
+    if (pos < 0) return false;
+    const int64_t ti = index0 + (pos >> sh);
+    if (ti < 0 || ti >= sd.index_len) return false;
+    blk = small != nullptr ? ld_const(small + ti)
+                           : ld_const(static_cast<const int32_t*>(sd.index) + ti);
+    if (blk < 0 || blk >= (cap >> sh)) return false;
+    off = pos & ((int64_t{1} << sh) - 1);
+  } else {
+    int64_t slot = pos0 + i;
+    if (sd.mode == MKV_ADDR_SLOTS) {
+      const int64_t ii = index0 + i;
+      if (ii < 0 || ii >= sd.index_len) return false;
+      slot = ld_const((small != nullptr ? small : static_cast<const int64_t*>(sd.index)) + ii);
+    }
+    if (slot < 0 || slot >= cap) return false;
+    blk = slot >> sh;
+    off = slot & ((int64_t{1} << sh) - 1);
+  }
+  off_bytes = blk * sd.bstride + off * sd.ostride;
+  return true;
+}
+
+// Wave-uniform: the span holding token g, the s with starts[s] <= g < starts[s + 1]
+// (n_spans <= 63): each lane reads one prefix entry, and a ballot counts the entries at
+// or below g.  -1 below the first span, n_spans past the last.  Every lane calls it.
+__device__ __forceinline__ int span_of(const int64_t* starts, int n_spans, int64_t g,
+                                       int lane) {
+  const int64_t v = lane <= n_spans ? starts[lane] : INT64_MAX;
+  return static_cast<int>(__popcll(__ballot(v <= g))) - 1;
+}
+
+// This lane's C cos / signed-sin values of a span's rotation, computed as the plan pass
+// computes its tables (fp32 angle, double-precision sincos, rounded to fp32).
+template <int C>
+__device__ __forceinline__ void lane_tables(int delta, const float* inv_freq, int rotary, int j,
+                                            float* cs, float* sg) {
+  const int half = rotary / 2;
+#pragma unroll
+  for (int e = 0; e < C; ++e) {
+    const int i = j * C + e;
+    const int f = i < half ? i : i - half;
+    const float ang = static_cast<float>(delta) * inv_freq[f];
+    double sd, cd;
+    sincos(static_cast<double>(ang), &sd, &cd);
+    cs[e] = static_cast<float>(cd);
+    sg[e] = i < half ? -static_cast<float>(sd) : static_cast<float>(sd);
+  }
+}
+
 // --------------------------------------------------------------------- plan kernel
 //
 // Every workgroup builds the token prefix over spans in LDS, then resolves a
@@ -550,8 +630,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
 // (token, head) rows.  UNIFORM: heads % rpw == 0, so every row of a pass belongs to
 // one token.
 
-template <int DT, bool BATCHED, bool UNIFORM>
-__global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
+template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, bool SMALL>
+__device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack* q) {
+  static_assert(!DIRECT || (BATCHED && UNIFORM), "direct shifts resolve one token per pass");
+  static_assert(!SMALL || DIRECT, "small shifts take the direct path");
   using E = Elem<DT>;
   constexpr int C = E::kPerChunk;
   constexpr int U = E::kPasses;
@@ -579,6 +661,20 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
     tile = (blockIdx.x % MKV_XCDS) * per + blockIdx.x / MKV_XCDS;
   }
   const int64_t g0 = tile * p.tile_tokens;
+  if constexpr (DIRECT && !SMALL) {
+    // one workgroup checks the caller's prefix against the span table: starts[0] == 0,
+    // each step equals the span's token count, and the last is at most total_tokens
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0 && p.err != nullptr) {
+      bool bad = false;
+      if (lane < p.n_spans) {
+        const int64_t lo = p.starts[lane], hi = p.starts[lane + 1];
+        const int32_t n = p.spans[lane].n_tokens;
+        bad = hi - lo != (n > 0 ? n : 0) || (lane == 0 && lo != 0) ||
+              (lane == p.n_spans - 1 && hi > p.total_tokens) || n < 0;
+      }
+      if (__ballot(bad) != 0 && lane == 0) atomicOr(p.err, MKV_FLAG_SPAN);
+    }
+  }
   const int64_t left = p.total_tokens - g0;
   if (left <= 0) return;  // padding workgroups of the XCD-aware grid
   const int ntok = static_cast<int>(left < p.tile_tokens ? left : p.tile_tokens);
@@ -638,7 +734,52 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       head_u[u] = rr - t * H;
       const int64_t g = g0 + t;
       live[u] = r < nrows;
-      if constexpr (BATCHED) {
+      if constexpr (DIRECT) {
+        // the token's span and rows, resolved here from the span table (no plan pass)
+        int s;
+        const int64_t* starts = SMALL ? q->starts : p.starts;
+        if constexpr (SMALL) {
+          s = -1;  // the prefix is the launch's own: a uniform scan of at most 9 entries
+#pragma unroll
+          for (int k = 0; k <= MKV_SMALL_MAX_SPANS; ++k)
+            if (k <= p.n_spans && q->starts[k] <= g) s = k;
+        } else {
+          s = span_of(p.starts, p.n_spans, g, lane);
+        }
+        const int sc = s >= 0 && s < p.n_spans ? s : 0;  // clamped: reads stay in range
+        const mkv_span_t* sp = (SMALL ? q->spans : p.spans) + sc;
+        const int64_t i = g - ld_const(starts + sc);
+        const int32_t sg = ld_const(&sp->src_group), dg = ld_const(&sp->dst_group);
+        const bool in_span = live[u] && s == sc && i >= 0;
+        bool ok = in_span && i < ld_const(&sp->n_tokens) && sg >= 0 && sg < p.src.groups &&
+                  dg >= 0 && dg < p.dst.groups;
+        int64_t so = 0, dof = 0;
+        if (ok) {
+          const int64_t s_cap = p.src.group_slots != nullptr ? ld_const(p.src.group_slots + sg)
+                                                             : p.src.num_slots;
+          const int64_t d_cap = p.dst.group_slots != nullptr ? ld_const(p.dst.group_slots + dg)
+                                                             : p.dst.num_slots;
+          const bool s_ok = resolve_direct(p.src, SMALL ? q->src_index : nullptr, s_cap,
+                                           ld_const(&sp->src_pos), ld_const(&sp->src_index), i,
+                                           so);
+          const bool d_ok = resolve_direct(p.dst, SMALL ? q->dst_index : nullptr, d_cap,
+                                           ld_const(&sp->dst_pos), ld_const(&sp->dst_index), i,
+                                           dof);
+          if (!(s_ok && d_ok)) {
+            if (p.err != nullptr && lane == 0)
+              atomicOr(p.err, (s_ok ? 0 : MKV_FLAG_SRC_RANGE) | (d_ok ? 0 : MKV_FLAG_DST_RANGE));
+            ok = false;
+          }
+        } else if (in_span && p.err != nullptr && lane == 0) {
+          atomicOr(p.err, MKV_FLAG_SPAN);  // a bad group, or a prefix the spans do not fill
+        }
+        span_u[u] = ok ? s : -1;
+        delta_u[u] = ld_const(&sp->delta);
+        s_at[u] = so;
+        d_at[u] = dof;
+        sb_u[u] = (ok ? sg : 0) * p.layers + layer;
+        db_u[u] = (ok ? dg : 0) * p.layers + layer;
+      } else if constexpr (BATCHED) {
         const TokRec* rp = p.recs + g;
         span_u[u] = UNIFORM ? ld_const(&rp->span) : rp->span;
         delta_u[u] = UNIFORM ? ld_const(&rp->delta) : rp->delta;
@@ -734,7 +875,8 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       // instead of being fetched after it.  A later pass of another span (rare) still
       // loads its own in phase C.  Measured +2-3% for fp8; for bf16, which runs at full
       // occupancy, 1-4% slower, so there the table follows the data.
-      if (live[0] && lane_live && rot_lane && delta_u[0] != 0 && span_u[0] != cur_span) {
+      if (!SMALL && live[0] && lane_live && rot_lane && delta_u[0] != 0 &&
+          span_u[0] != cur_span) {
         const float* tb = p.tables + static_cast<int64_t>(span_u[0]) * 2 * p.rotary;
 #pragma unroll
         for (int e = 0; e < C; ++e) {
@@ -768,11 +910,15 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       if (live[u] && lane_live && rot_lane && delta_u[u] != 0) {
         if constexpr (BATCHED) {
           if (span_u[u] != cur_span) {
-            const float* tb = p.tables + static_cast<int64_t>(span_u[u]) * 2 * p.rotary;
+            if constexpr (SMALL) {
+              lane_tables<C>(delta_u[u], p.inv_freq, p.rotary, j, cs, sg);
+            } else {
+              const float* tb = p.tables + static_cast<int64_t>(span_u[u]) * 2 * p.rotary;
 #pragma unroll
-            for (int e = 0; e < C; ++e) {
-              cs[e] = tb[j * C + e];
-              sg[e] = tb[p.rotary + j * C + e];
+              for (int e = 0; e < C; ++e) {
+                cs[e] = tb[j * C + e];
+                sg[e] = tb[p.rotary + j * C + e];
+              }
             }
             cur_span = span_u[u];
           }
@@ -800,6 +946,17 @@ __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
       }
     }
   }
+}
+
+template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT>
+__global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
+  shift_body<DT, BATCHED, UNIFORM, DIRECT, false>(p, nullptr);
+}
+
+// A small shift: the span table, prefix and index windows arrive in the arguments.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void shift_small_kernel(SmallParams a) {
+  shift_body<DT, true, true, true, true>(a.p, &a.q);
 }
 
 // --------------------------------------------------------------------- host side
@@ -916,7 +1073,7 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_
   return MKV_OK;
 }
 
-template <int DT, bool BATCHED, bool UNIFORM>
+template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT>
 int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t stream) {
   // tiles is rounded up to a multiple of MKV_XCDS below; extra workgroups exit at once
   if (tiles <= 0) return MKV_OK;
@@ -924,7 +1081,7 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
   if (tiles > 0x7FFFFFFF || layers > 65535)
     return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
                 layers);
-  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM>),
+  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT>),
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
                      dim3(kThreads), 0, stream, sp);
   const hipError_t e = hipGetLastError();
@@ -933,12 +1090,14 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
 }
 
 template <bool BATCHED>
-int launch_any(int dtype, bool uniform, const ShiftParams& sp, int64_t tiles, int layers,
-               hipStream_t stream) {
-#define MKV_CASE(DT)                                                             \
-  case DT:                                                                       \
-    return uniform ? launch_shift<DT, BATCHED, true>(sp, tiles, layers, stream)  \
-                   : launch_shift<DT, BATCHED, false>(sp, tiles, layers, stream);
+int launch_any(int dtype, bool uniform, bool direct, const ShiftParams& sp, int64_t tiles,
+               int layers, hipStream_t stream) {
+#define MKV_CASE(DT)                                                                     \
+  case DT:                                                                               \
+    if (BATCHED && uniform && direct)                                                    \
+      return launch_shift<DT, BATCHED, BATCHED, BATCHED>(sp, tiles, layers, stream);    \
+    return uniform ? launch_shift<DT, BATCHED, true, false>(sp, tiles, layers, stream)   \
+                   : launch_shift<DT, BATCHED, false, false>(sp, tiles, layers, stream);
   switch (dtype) {
     MKV_CASE(MKV_BF16)
     MKV_CASE(MKV_F16)
@@ -1092,7 +1251,8 @@ extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
   sp.heads_magic = g.heads_magic;
   sp.rotate = rot ? 1 : 0;
   const int64_t tiles = (n_tokens + g.tile_tokens - 1) / g.tile_tokens;
-  return launch_any<false>(dtype, g.uniform, sp, tiles, 1, static_cast<hipStream_t>(stream));
+  return launch_any<false>(dtype, g.uniform, false, sp, tiles, 1,
+                           static_cast<hipStream_t>(stream));
 }
 
 namespace {
@@ -1120,8 +1280,46 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   if (d->src.k_base == nullptr || d->src.v_base == nullptr || d->dst.k_base == nullptr ||
       d->dst.v_base == nullptr)
     return fail(MKV_ERR_ARG, "NULL base-address table");
-  const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t tiles = (d->total_tokens + g.tile_tokens - 1) / g.tile_tokens;
+  if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "total_tokens too large");
+
+  ShiftParams sp;
+  memset(&sp, 0, sizeof sp);
+  sp.src_k_base = d->src.k_base;
+  sp.src_v_base = d->src.v_base;
+  sp.dst_k_base = d->dst.k_base;
+  sp.dst_v_base = d->dst.v_base;
+  sp.k_scale = d->k_scale;
+  sp.err = d->error_flags;
+  sp.total_tokens = d->total_tokens;
+  sp.layers = d->layers;
+  sp.heads = d->heads;
+  sp.rotary = d->rotary;
+  sp.tile_tokens = g.tile_tokens;
+  sp.chunks_per_row = g.chunks_per_row;
+  sp.rows_per_wave = g.rows_per_wave;
+  sp.heads_magic = g.heads_magic;
+
+  // one launch and no workspace: the shift kernel resolves every token from the span
+  // table, the caller's token prefix and the caller's per-span tables
+  if (d->span_starts != nullptr && d->span_tables != nullptr && g.uniform &&
+      d->n_spans <= MKV_DIRECT_MAX_SPANS && ilog2_exact(d->src.block_size) >= 0 &&
+      ilog2_exact(d->dst.block_size) >= 0) {
+    if (!aligned16(reinterpret_cast<uint64_t>(d->span_tables)))
+      return fail(MKV_ERR_ALIGN, "span_tables not 16-byte aligned");
+    rc = make_side(d->src, eb, sp.src, sp.src_hstride, "src");
+    if (rc != MKV_OK) return rc;
+    rc = make_side(d->dst, eb, sp.dst, sp.dst_hstride, "dst");
+    if (rc != MKV_OK) return rc;
+    sp.spans = d->spans;
+    sp.starts = d->span_starts;
+    sp.n_spans = d->n_spans;
+    sp.tables = d->span_tables;
+    return launch_any<true>(d->dtype, true, true, sp, tiles, d->layers, st);
+  }
+
+  const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary);
   void* ws_ptr = d->workspace;
   int64_t ws_bytes = d->workspace_bytes;
   if (noalloc) {
@@ -1139,8 +1337,6 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
                 (long long)need);
   if (!aligned16(reinterpret_cast<uint64_t>(ws_ptr)))
     return fail(MKV_ERR_ALIGN, "workspace not 16-byte aligned");
-  const int64_t tiles = (d->total_tokens + g.tile_tokens - 1) / g.tile_tokens;
-  if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "total_tokens too large");
 
   PlanParams pp;
   memset(&pp, 0, sizeof pp);
@@ -1175,19 +1371,106 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "plan launch failed: %s", hipGetErrorString(e));
 
-  ShiftParams sp;
-  memset(&sp, 0, sizeof sp);
   sp.recs = recs;
   sp.tables = tables;
+  sp.src_hstride = src_hs;
+  sp.dst_hstride = dst_hs;
+  return launch_any<true>(d->dtype, g.uniform, false, sp, tiles, d->layers, st);
+}
+
+template <int DT>
+int launch_small(const SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
+  tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
+  hipLaunchKernelGGL(shift_small_kernel<DT>,
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
+                     dim3(kThreads), 0, stream, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
+  return MKV_OK;
+}
+
+// One side's index window, from the caller's host array into the launch's int64 window.
+int pack_index(const mkv_side_t& in, int64_t* out, const char* name) {
+  if (in.mode == MKV_ADDR_FLAT) return MKV_OK;
+  if (in.index_len < 0 || in.index_len > MKV_SMALL_MAX_INDEX)
+    return fail(MKV_ERR_UNSUPPORTED, "%s: index of %lld entries, more than %d for a small shift",
+                name, (long long)in.index_len, MKV_SMALL_MAX_INDEX);
+  if (in.index_len > 0 && in.index == nullptr) return fail(MKV_ERR_ARG, "%s: index is NULL", name);
+  for (int64_t k = 0; k < in.index_len; ++k)
+    out[k] = in.mode == MKV_ADDR_TABLE ? static_cast<const int32_t*>(in.index)[k]
+                                       : static_cast<const int64_t*>(in.index)[k];
+  return MKV_OK;
+}
+
+}  // namespace
+
+extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
+  return shift_spans(d, stream, false);
+}
+
+extern "C" int mkv_shift_spans_small(const mkv_shift_desc_t* d, void* stream) {
+  g_err[0] = '\0';
+  if (d == nullptr) return fail(MKV_ERR_ARG, "NULL descriptor");
+  const int eb = elem_bytes(d->dtype);
+  if (eb == 0) return fail(MKV_ERR_DTYPE, "unknown dtype %d", d->dtype);
+  Geometry g;
+  int rc = check_geometry(d->dtype, d->heads, d->head_size, d->rotary,
+                          d->src.head_stride * eb, d->dst.head_stride * eb, g);
+  if (rc != MKV_OK) return rc;
+  if (d->n_spans < 0 || d->n_spans > MKV_SMALL_MAX_SPANS)
+    return fail(MKV_ERR_UNSUPPORTED, "n_spans %d outside [0, %d] for a small shift", d->n_spans,
+                MKV_SMALL_MAX_SPANS);
+  if (d->total_tokens < 0) return fail(MKV_ERR_ARG, "total_tokens < 0");
+  if (d->n_spans == 0 || d->total_tokens == 0) return MKV_OK;
+  if (d->spans == nullptr) return fail(MKV_ERR_ARG, "NULL span table");
+  if (d->layers <= 0) return fail(MKV_ERR_ARG, "layers %d", d->layers);
+  if (d->rotary > 0 && d->inv_freq == nullptr) return fail(MKV_ERR_ARG, "inv_freq is NULL");
+  if (d->dtype == MKV_FP8_E4M3 && d->rotary > 0 && d->k_scale == nullptr)
+    return fail(MKV_ERR_ARG, "fp8 needs k_scale");
+  if (d->src.k_base == nullptr || d->src.v_base == nullptr || d->dst.k_base == nullptr ||
+      d->dst.v_base == nullptr)
+    return fail(MKV_ERR_ARG, "NULL base-address table");
+  if (!g.uniform || ilog2_exact(d->src.block_size) < 0 || ilog2_exact(d->dst.block_size) < 0)
+    return fail(MKV_ERR_UNSUPPORTED,
+                "a small shift needs power-of-two block sizes and heads a multiple of %d",
+                g.rows_per_wave);
+  const int64_t tiles = (d->total_tokens + g.tile_tokens - 1) / g.tile_tokens;
+  if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "total_tokens too large");
+
+  static thread_local SmallParams a;  // ~2 KB: kept off the stack, rewritten every call
+  memset(&a, 0, sizeof a);
+  int64_t acc = 0;
+  for (int k = 0; k < d->n_spans; ++k) {
+    a.q.spans[k] = d->spans[k];
+    if (d->spans[k].n_tokens < 0)
+      return fail(MKV_ERR_ARG, "span %d has n_tokens %d", k, d->spans[k].n_tokens);
+    a.q.starts[k] = acc;
+    acc += d->spans[k].n_tokens;
+  }
+  for (int k = d->n_spans; k <= MKV_SMALL_MAX_SPANS; ++k) a.q.starts[k] = acc;
+  if (acc > d->total_tokens)
+    return fail(MKV_ERR_ARG, "the spans hold %lld tokens, total_tokens is %lld", (long long)acc,
+                (long long)d->total_tokens);
+  rc = pack_index(d->src, a.q.src_index, "src");
+  if (rc != MKV_OK) return rc;
+  rc = pack_index(d->dst, a.q.dst_index, "dst");
+  if (rc != MKV_OK) return rc;
+
+  ShiftParams& sp = a.p;
+  rc = make_side(d->src, eb, sp.src, sp.src_hstride, "src");
+  if (rc != MKV_OK) return rc;
+  rc = make_side(d->dst, eb, sp.dst, sp.dst_hstride, "dst");
+  if (rc != MKV_OK) return rc;
+  sp.src.index = nullptr;  // host arrays: the kernel reads the launch's own windows
+  sp.dst.index = nullptr;
   sp.src_k_base = d->src.k_base;
   sp.src_v_base = d->src.v_base;
   sp.dst_k_base = d->dst.k_base;
   sp.dst_v_base = d->dst.v_base;
   sp.k_scale = d->k_scale;
+  sp.inv_freq = d->inv_freq;
   sp.err = d->error_flags;
   sp.total_tokens = d->total_tokens;
-  sp.src_hstride = src_hs;
-  sp.dst_hstride = dst_hs;
   sp.layers = d->layers;
   sp.heads = d->heads;
   sp.rotary = d->rotary;
@@ -1195,13 +1478,18 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   sp.chunks_per_row = g.chunks_per_row;
   sp.rows_per_wave = g.rows_per_wave;
   sp.heads_magic = g.heads_magic;
-  return launch_any<true>(d->dtype, g.uniform, sp, tiles, d->layers, st);
-}
-
-}  // namespace
-
-extern "C" int mkv_shift_spans(const mkv_shift_desc_t* d, void* stream) {
-  return shift_spans(d, stream, false);
+  sp.n_spans = d->n_spans;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (d->dtype) {
+    case MKV_BF16:
+      return launch_small<MKV_BF16>(a, tiles, d->layers, st);
+    case MKV_F16:
+      return launch_small<MKV_F16>(a, tiles, d->layers, st);
+    case MKV_F32:
+      return launch_small<MKV_F32>(a, tiles, d->layers, st);
+    default:
+      return launch_small<MKV_FP8_E4M3>(a, tiles, d->layers, st);
+  }
 }
 
 extern "C" int mkv_shift_spans_noalloc(const mkv_shift_desc_t* d, void* stream) {

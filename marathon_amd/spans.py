@@ -28,6 +28,30 @@ from .shift_kernels import current_stream, dtype_code
 
 MODES = {"flat": _lib.MKV_ADDR_FLAT, "slots": _lib.MKV_ADDR_SLOTS, "table": _lib.MKV_ADDR_TABLE}
 
+#: Shifts of at most this many (token, layer) rows take the library's direct path when
+#: eligible: one launch instead of the plan pass plus the shift.  Measured on MI355X
+#: (bf16, 8 heads, 40 layers): 1 and 16 tokens run in 6.8 and 7.1 us direct against
+#: 9.1 and 9.9 us; from 512 tokens the two-launch path is faster (0.036 against
+#: 0.043 ms), and at 8,192 tokens it streams 6.2 TB/s against 4.4, because a direct
+#: workgroup resolves its token through four dependent metadata reads before its data.
+DIRECT_MAX_TOKEN_LAYERS = 4096
+
+
+class _on:
+    """``torch.cuda.device(device)`` only when ``device`` is not already current."""
+
+    def __init__(self, device, current: bool):
+        self.ctx = None if current else torch.cuda.device(device)
+
+    def __enter__(self):
+        if self.ctx is not None:
+            self.ctx.__enter__()
+
+    def __exit__(self, *exc):
+        if self.ctx is not None:
+            return self.ctx.__exit__(*exc)
+        return False
+
 
 @dataclass
 class CacheSet:
@@ -138,6 +162,25 @@ class CacheSet:
             got = self._bases = (k, v, caps, int(caps.min()), bool(np.all(caps == caps[0])))
         return got
 
+    def device_tables(self, device) -> tuple:
+        """``(k_ptr, v_ptr, caps_ptr or None, ready)``: the base-address tables (and the
+        per-group capacities, when they differ) on ``device``, uploaded once per CacheSet
+        with one stream-ordered copy on the current stream; ``ready`` is an event after
+        that copy, for launches on other streams.  The upload is kept alive by the set."""
+        got = getattr(self, "_dev", None)
+        if got is None:
+            k, v, caps, _, uniform = self.base_tables()
+            stage = _Staging()
+            offs = (stage.add(k.reshape(-1)), stage.add(v.reshape(-1)),
+                    None if uniform else stage.add(caps))
+            blob = stage.upload(device)
+            ready = torch.cuda.Event()
+            ready.record()
+            base = blob.data_ptr()
+            got = self._dev = (base + offs[0], base + offs[1],
+                               None if offs[2] is None else base + offs[2], ready, blob)
+        return got
+
 
 class _Staging:
     """Host arrays bound for the device, packed into one pinned buffer and copied with
@@ -176,6 +219,11 @@ class ShiftPlan:
     Everything host-side (span table, per-(group, layer) base addresses, host index
     arrays, tables) goes to the device in one pinned, stream-ordered copy, so building
     a plan never blocks on the GPU.
+
+    ``direct``: None (default) takes the library's single-launch path whenever
+    :meth:`direct_eligible` allows it, with the token prefix and the per-span rotation
+    tables computed here (:func:`span_tables`); False always runs the two-launch path
+    (plan pass and workspace), True asks for the direct path where eligible.
     """
 
     def __init__(
@@ -190,6 +238,7 @@ class ShiftPlan:
         dst_mode: str = "slots",
         dst_index: torch.Tensor | None = None,
         k_scale: torch.Tensor | None = None,
+        direct: bool | None = None,
     ):
         spans = np.ascontiguousarray(np.asarray(spans, dtype=_lib.SPAN_DTYPE))
         if src.layers != dst.layers:
@@ -234,22 +283,36 @@ class ShiftPlan:
             if scale[2] < dst.layers:
                 raise ValueError("k_scale needs one entry per layer")
 
-        src_plan = self._side(src, src_mode, src_index, stage, place)
-        dst_plan = self._side(dst, dst_mode, dst_index, stage, place)
+        for mode in (src_mode, dst_mode):
+            if mode not in MODES:
+                raise ValueError(f"mode {mode!r}")
+        src_index = self._index(src_mode, src_index, place)
+        dst_index = self._index(dst_mode, dst_index, place)
         span_off = stage.add(spans.view(np.uint8).reshape(-1)) if self.n_spans else None
-        # the tables are copied on the device's current stream; a launch on another
-        # stream first waits for this event (see _launch)
-        if self.device.index == torch.cuda.current_device():
+        # the direct path (one launch, no workspace) for small shifts, where the plan
+        # pass's launch dominates; the token prefix and per-span tables come from here
+        if direct is None:
+            direct = self.tokens * dst.layers <= DIRECT_MAX_TOKEN_LAYERS
+        self.direct = bool(direct) and self.direct_eligible(src, dst, self.n_spans)
+        starts_off = tables_off = None
+        if self.direct:
+            starts_off = stage.add(np.concatenate(([0], np.cumsum(counts))).astype(np.int64))
+            tables_off = stage.add(span_tables(spans["delta"], inv_freq, self.rotary))
+
+        on_device = self.device.index == torch.cuda.current_device()
+        with _on(self.device, on_device):
+            # the caches' base-address tables: uploaded once per CacheSet
+            self._tables_ready = []
+            sides = []
+            for cs in (src, dst):
+                k_ptr, v_ptr, caps_ptr, ready, _ = cs.device_tables(self.device)
+                self._tables_ready.append(ready)
+                sides.append((k_ptr, v_ptr, caps_ptr))
+            # this plan's own arrays: one stream-ordered copy on the current stream
             blob = stage.upload(self.device)
-            self._ready = torch.cuda.Event()
-            self._ready.record()
-        else:
-            with torch.cuda.device(self.device):
-                blob = stage.upload(self.device)
-                self._ready = torch.cuda.Event()
-                self._ready.record()
+            self._build_stream = current_stream(self.device)
         self._keep.append(blob)
-        self._synced = {current_stream(self.device)}
+        self._synced = {self._build_stream}
         base = blob.data_ptr()
 
         def ptr(item) -> int | None:
@@ -258,25 +321,32 @@ class ShiftPlan:
                 return t.data_ptr()
             return None if off is None else base + off
 
-        src_side = self._finish_side(src_plan, ptr)
-        dst_side = self._finish_side(dst_plan, ptr)
+        src_side = self._make_side(src, src_mode, src_index, sides[0], ptr)
+        dst_side = self._make_side(dst, dst_mode, dst_index, sides[1], ptr)
 
         self.descs = []
         step = _lib.MKV_MAX_SPANS
         chunks = [(lo, min(step, self.n_spans - lo)) for lo in range(0, self.n_spans, step)]
-        L = _lib.lib()
-        need = max(
-            (L.mkv_shift_workspace_size(sum(counts[lo:lo + cnt]), cnt, self.rotary)
-             for lo, cnt in chunks),
-            default=0,
-        )
-        # one workspace serves every chunk: the chunks run in stream order
-        self.workspace = torch.empty(max(int(need), 16), dtype=torch.uint8, device=self.device)
+        self.workspace = None
+        if not self.direct:
+            L = _lib.lib()
+            need = max(
+                (L.mkv_shift_workspace_size(sum(counts[lo:lo + cnt]), cnt, self.rotary)
+                 for lo, cnt in chunks),
+                default=0,
+            )
+            # one workspace serves every chunk: the chunks run in stream order
+            self.workspace = torch.empty(max(int(need), 16), dtype=torch.uint8,
+                                         device=self.device)
         for lo, cnt in chunks:
             d = _lib.ShiftDesc()
             d.spans = base + span_off + lo * _lib.SPAN_DTYPE.itemsize
-            d.workspace = self.workspace.data_ptr()
-            d.workspace_bytes = self.workspace.numel()
+            if self.direct:  # a single chunk
+                d.span_starts = base + starts_off
+                d.span_tables = base + tables_off
+            else:
+                d.workspace = self.workspace.data_ptr()
+                d.workspace_bytes = self.workspace.numel()
             d.total_tokens = sum(counts[lo:lo + cnt])
             d.inv_freq = ptr(inv)
             d.k_scale = ptr(scale)
@@ -292,43 +362,40 @@ class ShiftPlan:
             self.descs.append(d)
 
     @staticmethod
-    def _side(cs: CacheSet, mode: str, index, stage: _Staging, place) -> dict:
-        if mode not in MODES:
-            raise ValueError(f"mode {mode!r}")
-        k, v, caps, min_cap, uniform = cs.base_tables()
-        out = {
-            "cs": cs,
-            "mode": mode,
-            "k": (None, stage.add(k.reshape(-1)), k.size),
-            "v": (None, stage.add(v.reshape(-1)), v.size),
-            "num_slots": min_cap,
-            "group_slots": None if uniform else (None, stage.add(caps), caps.size),
-            "index": (None, None, 0),
-        }
-        if mode != "flat":
-            if index is None:
-                raise ValueError(f"mode {mode!r} needs an index array")
-            if mode == "slots":
-                out["index"] = place(index, torch.int64, np.int64)
-            else:
-                out["index"] = place(index, torch.int32, np.int32)
-        return out
+    def direct_eligible(src: CacheSet, dst: CacheSet, n_spans: int) -> bool:
+        """Whether the library takes the direct path for this shift: at most
+        ``MKV_DIRECT_MAX_SPANS`` spans, power-of-two block sizes on both sides, and a
+        head count that is a multiple of the rows one wave covers (every row of a wave
+        pass then belongs to one token)."""
+        eb = dst.first.element_size()
+        rows_per_wave = 64 // max(1, dst.head_size * eb // 16)
+        pow2 = all(cs.block_size > 0 and cs.block_size & (cs.block_size - 1) == 0
+                   for cs in (src, dst))
+        return (0 < n_spans <= _lib.MKV_DIRECT_MAX_SPANS and pow2
+                and dst.heads % rows_per_wave == 0)
 
     @staticmethod
-    def _finish_side(plan: dict, ptr) -> _lib.Side:
-        cs = plan["cs"]
+    def _index(mode: str, index, place):
+        if mode == "flat":
+            return None, None, 0
+        if index is None:
+            raise ValueError(f"mode {mode!r} needs an index array")
+        if mode == "slots":
+            return place(index, torch.int64, np.int64)
+        return place(index, torch.int32, np.int32)
+
+    @staticmethod
+    def _make_side(cs: CacheSet, mode: str, index, tables: tuple, ptr) -> _lib.Side:
         side = _lib.Side()
-        side.k_base = ptr(plan["k"])
-        side.v_base = ptr(plan["v"])
-        side.num_slots = plan["num_slots"]
-        side.group_slots = None if plan["group_slots"] is None else ptr(plan["group_slots"])
-        n_index = plan["index"][2]
-        side.index = ptr(plan["index"]) if n_index else None
+        side.k_base, side.v_base, side.group_slots = tables
+        side.num_slots = cs.base_tables()[3]
+        n_index = index[2]
+        side.index = ptr(index) if n_index else None
         side.index_len = n_index
         bs, hstr, ostr = cs.strides
         side.block_stride, side.head_stride, side.offset_stride = bs, hstr, ostr
         side.block_size = cs.block_size
-        side.mode = MODES[plan["mode"]]
+        side.mode = MODES[mode]
         side.groups = cs.groups
         return side
 
@@ -357,17 +424,202 @@ class ShiftPlan:
     def _launch(self, stream: int, error_flags: torch.Tensor | None) -> None:
         L = _lib.lib()
         if stream not in self._synced:
-            # the tables were copied on the stream current at build time
+            # the plan's arrays were copied on the stream current at build time, the
+            # caches' base-address tables when each set was first used
             ext = torch.cuda.ExternalStream(stream, device=self.device)
             if not torch.cuda.is_current_stream_capturing():
-                ext.wait_event(self._ready)
-            for t in (*self._keep, self.workspace):
+                ext.wait_stream(torch.cuda.ExternalStream(self._build_stream,
+                                                          device=self.device))
+                for ready in self._tables_ready:
+                    ext.wait_event(ready)
+            for t in self._keep + ([] if self.workspace is None else [self.workspace]):
                 t.record_stream(ext)
             self._synced.add(stream)
         flags = error_flags.data_ptr() if error_flags is not None else None
         for d in self.descs:
             d.error_flags = flags
             _lib.check(L.mkv_shift_spans(ctypes.byref(d), ctypes.c_void_p(stream)))
+
+
+class SmallShifts:
+    """Direct-path shifts of a few tokens, with no per-step allocation or descriptor
+    building: the steady state of a serving loop (a decode step's saves, short loads).
+
+    One device buffer per (source caches, destination caches, addressing modes) holds a
+    step's span table, token prefix, rotation tables and index windows; :meth:`run`
+    rewrites it with one pinned copy on the current stream and launches the step with a
+    descriptor kept from the previous one.  Stream order keeps a step's copy after the
+    previous step's kernel, which still reads the buffer.  Only steps that take the
+    library's direct path come here (:meth:`fits`); the rest build a :class:`ShiftPlan`.
+    """
+
+    SPANS_AT = 0
+    STARTS_AT = _lib.MKV_DIRECT_MAX_SPANS * _lib.SPAN_DTYPE.itemsize  # 3,024 B
+    TABLES_AT = STARTS_AT + 64 * 8
+
+    def __init__(self, src: CacheSet, dst: CacheSet, *, inv_freq: torch.Tensor | None,
+                 src_mode: str, dst_mode: str, k_scale: torch.Tensor | None = None):
+        self.src, self.dst = src, dst
+        self.device = dst.first.device
+        self.rotary = 0 if inv_freq is None else 2 * int(inv_freq.numel())
+        self.inv_host = None if inv_freq is None else inv_freq.detach().to(
+            "cpu", torch.float32).contiguous()
+        self.dtype = dtype_code(dst.first.dtype)
+        self.modes = (src_mode, dst_mode)
+        self.eligible_geometry = ShiftPlan.direct_eligible(src, dst, 1)
+        self._idx = {"flat": (None, 0), "slots": (np.int64, 8), "table": (np.int32, 4)}
+        self.capacity = 0
+        self.buf = None
+        self._keep = []
+        with _on(self.device, self.device.index == torch.cuda.current_device()):
+            static = _Staging()
+            inv_off = None if inv_freq is None else static.add(self.inv_host.numpy())
+            scale_off = None
+            if self.dtype == _lib.MKV_FP8_E4M3 and self.rotary:
+                if k_scale is None:
+                    raise ValueError("fp8 caches need k_scale [layers]")
+                scale = k_scale.detach().to("cpu", torch.float32).reshape(-1).numpy()
+                if scale.size < dst.layers:
+                    raise ValueError("k_scale needs one entry per layer")
+                scale_off = static.add(scale)
+            blob = static.upload(self.device)
+            self._keep.append(blob)
+            sides = [cs.device_tables(self.device)[:3] for cs in (src, dst)]
+        base = blob.data_ptr()
+        d = self.desc = _lib.ShiftDesc()
+        d.inv_freq = None if inv_off is None else base + inv_off
+        d.k_scale = None if scale_off is None else base + scale_off
+        d.layers, d.heads, d.head_size = dst.layers, dst.heads, dst.head_size
+        d.rotary, d.dtype = self.rotary, self.dtype
+        d.src = ShiftPlan._make_side(src, src_mode, (None, None, 0), sides[0], None)
+        d.dst = ShiftPlan._make_side(dst, dst_mode, (None, None, 0), sides[1], None)
+        # the same shift for mkv_shift_spans_small: host span rows and index windows
+        self.small_desc = _lib.ShiftDesc()
+        ctypes.memmove(ctypes.byref(self.small_desc), ctypes.byref(d), ctypes.sizeof(d))
+        self._last: tuple = ()
+        self.tokens = 0
+
+    def fits(self, n_spans: int, tokens: int) -> bool:
+        return (self.eligible_geometry and 0 < n_spans <= _lib.MKV_DIRECT_MAX_SPANS
+                and tokens * self.dst.layers <= DIRECT_MAX_TOKEN_LAYERS)
+
+    def _ensure(self, nbytes: int) -> None:
+        if nbytes > self.capacity:
+            self.capacity = max(nbytes, 2 * self.capacity, self.TABLES_AT + 4096)
+            self.buf = torch.empty(self.capacity, dtype=torch.uint8, device=self.device)
+            base = self.buf.data_ptr()
+            self.desc.spans = base + self.SPANS_AT
+            self.desc.span_starts = base + self.STARTS_AT
+            self.desc.span_tables = base + self.TABLES_AT
+
+    def run(self, rows: list, src_index: np.ndarray | None, dst_index: np.ndarray | None,
+            error_flags: torch.Tensor | None = None) -> None:
+        """Shift ``rows`` (``mkv_span_t`` field tuples) on the current stream, their
+        source and destination indices given as host arrays (None for ``flat``).
+
+        Up to ``MKV_SMALL_MAX_SPANS`` spans and ``MKV_SMALL_MAX_INDEX`` index entries a
+        side, the rows and windows travel in the launch itself
+        (``mkv_shift_spans_small``); beyond that they are copied into this runner's
+        device buffer first."""
+        n = len(rows)
+        n_src = 0 if src_index is None else src_index.size
+        n_dst = 0 if dst_index is None else dst_index.size
+        if (n <= _lib.MKV_SMALL_MAX_SPANS and n_src <= _lib.MKV_SMALL_MAX_INDEX
+                and n_dst <= _lib.MKV_SMALL_MAX_INDEX):
+            src_t, _ = self._idx[self.modes[0]]
+            dst_t, _ = self._idx[self.modes[1]]
+            spans = np.array(rows, dtype=_lib.SPAN_DTYPE)
+            si = None if not n_src else np.ascontiguousarray(src_index, dtype=src_t)
+            di = None if not n_dst else np.ascontiguousarray(dst_index, dtype=dst_t)
+            d = self.small_desc
+            d.spans = spans.ctypes.data
+            d.n_spans = n
+            d.total_tokens = self.tokens = sum(max(int(r[4]), 0) for r in rows)
+            d.src.index = None if si is None else si.ctypes.data
+            d.src.index_len = n_src
+            d.dst.index = None if di is None else di.ctypes.data
+            d.dst.index_len = n_dst
+            self._last = (spans, si, di)  # a relaunch reads them again
+            self.launch(error_flags=error_flags)
+            return
+        self._last = ()
+        spans = np.array(rows, dtype=_lib.SPAN_DTYPE)
+        counts = np.maximum(spans["n_tokens"], 0).astype(np.int64)
+        starts = np.zeros(n + 1, np.int64)
+        np.cumsum(counts, out=starts[1:])
+        src_t, src_b = self._idx[self.modes[0]]
+        dst_t, dst_b = self._idx[self.modes[1]]
+        # layout: span rows, prefix, the rotated spans' tables (when any), the indices
+        tables = None
+        if self.rotary and bool(spans["delta"].any()):
+            tables = span_tables(spans["delta"], self.inv_host, self.rotary)
+        src_at = self.TABLES_AT + (0 if tables is None else (tables.nbytes + 15) // 16 * 16)
+        dst_at = src_at + (n_src * src_b + 15) // 16 * 16
+        end = dst_at + n_dst * dst_b
+        self._ensure(end)
+        host = torch.empty(end, dtype=torch.uint8, pin_memory=True)
+        hv = host.numpy()
+        hv[self.SPANS_AT:self.SPANS_AT + spans.nbytes] = spans.view(np.uint8)
+        hv[self.STARTS_AT:self.STARTS_AT + starts.nbytes] = starts.view(np.uint8)
+        if tables is not None:
+            hv[self.TABLES_AT:self.TABLES_AT + tables.nbytes] = tables.reshape(-1).view(np.uint8)
+        if n_src:
+            hv[src_at:src_at + n_src * src_b] = np.ascontiguousarray(
+                src_index, dtype=src_t).view(np.uint8)
+        if n_dst:
+            hv[dst_at:dst_at + n_dst * dst_b] = np.ascontiguousarray(
+                dst_index, dtype=dst_t).view(np.uint8)
+        # one copy of the step's region (the gaps between parts are never read)
+        self.buf[:end].copy_(host, non_blocking=True)
+        d = self.desc
+        base = self.buf.data_ptr()
+        d.src.index = base + src_at if n_src else None
+        d.src.index_len = n_src
+        d.dst.index = base + dst_at if n_dst else None
+        d.dst.index_len = n_dst
+        d.n_spans = n
+        d.total_tokens = self.tokens = int(starts[-1])
+        self.launch(error_flags=error_flags)
+
+    def launch(self, stream: int | None = None, error_flags: torch.Tensor | None = None) -> None:
+        """(Re)launch the last step on ``stream`` (default: current); a step that went
+        through the device buffer must run on the stream it was copied on."""
+        small = bool(self._last)
+        d = self.small_desc if small else self.desc
+        d.error_flags = None if error_flags is None else error_flags.data_ptr()
+        if stream is None:
+            stream = current_stream(self.device)
+        L = _lib.lib()
+        fn = L.mkv_shift_spans_small if small else L.mkv_shift_spans
+        _lib.check(fn(ctypes.byref(d), ctypes.c_void_p(int(stream))))
+
+    @property
+    def direct(self) -> bool:
+        return True
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        eb = self.dst.first.element_size()
+        return 2 * self.tokens * self.dst.layers * self.dst.heads * 2 * self.dst.head_size * eb
+
+
+def span_tables(deltas, inv_freq: torch.Tensor | None, rotary: int) -> np.ndarray:
+    """Per-span rotation tables, fp32 ``[n_spans, 2, rotary]``: the cos of each element's
+    angle, then its signed sine (-sin on the first half, +sin on the second), where the
+    angle of frequency f is ``fl32(fl32(delta) * inv_freq[f])`` and cos/sin are its exact
+    values rounded once to fp32 (evaluated in float64) -- the tables the plan pass
+    computes on the device (shift_kernels.py:68-84 for the layout)."""
+    deltas = np.asarray(deltas, dtype=np.int64)
+    out = np.zeros((deltas.size, 2, rotary), np.float32)
+    if rotary == 0 or deltas.size == 0:
+        return out
+    inv = inv_freq.detach().to(device="cpu", dtype=torch.float32).numpy().reshape(-1)
+    ang = deltas.astype(np.float32)[:, None] * inv[None, :]  # fp32 products, rounded once
+    c = np.cos(ang.astype(np.float64)).astype(np.float32)
+    sn = np.sin(ang.astype(np.float64)).astype(np.float32)
+    out[:, 0, :] = np.concatenate((c, c), axis=1)
+    out[:, 1, :] = np.concatenate((-sn, sn), axis=1)
+    return out
 
 
 def span_array(rows) -> np.ndarray:

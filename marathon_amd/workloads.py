@@ -147,7 +147,7 @@ class Workload:
     v_scale: torch.Tensor | None = None
     meta: dict = field(default_factory=dict)
 
-    def plan(self) -> ShiftPlan:
+    def plan(self, direct: bool | None = None) -> ShiftPlan:
         return ShiftPlan(
             self.spans,
             self.src,
@@ -158,6 +158,7 @@ class Workload:
             dst_mode=self.dst_mode,
             dst_index=self.dst_index,
             k_scale=self.k_scale,
+            direct=direct,
         )
 
     @property

@@ -61,6 +61,7 @@ int main(void) {
   O(mkv_shift_desc_t, n_spans); O(mkv_shift_desc_t, layers);
   O(mkv_shift_desc_t, heads); O(mkv_shift_desc_t, head_size); O(mkv_shift_desc_t, rotary);
   O(mkv_shift_desc_t, dtype); O(mkv_shift_desc_t, src); O(mkv_shift_desc_t, dst);
+  O(mkv_shift_desc_t, span_starts); O(mkv_shift_desc_t, span_tables);
   return 0;
 }
 """
@@ -170,6 +171,42 @@ def test_noalloc_entry_point_refuses_shifts_beyond_its_scratch_without_a_gpu():
     assert b"no-allocation scratch" in lib.mkv_last_error()
     d.n_spans = 0  # an empty shift is a no-op, as for mkv_shift_spans
     assert lib.mkv_shift_spans_noalloc(ctypes.byref(d), None) == _lib.MKV_OK
+
+
+def test_small_entry_point_checks_its_limits_without_a_gpu():
+    """mkv_shift_spans_small refuses what does not fit a launch's arguments, and spans
+    that disagree with total_tokens, before any HIP call."""
+    import numpy as np
+
+    lib = _lib.lib()
+    d = _lib.ShiftDesc()
+    d.heads, d.head_size, d.rotary, d.dtype, d.layers = 8, 128, 128, _lib.MKV_BF16, 2
+    d.inv_freq = 1 << 21
+    for side in (d.src, d.dst):
+        side.k_base, side.v_base = 1 << 24, 1 << 25
+        side.mode, side.block_size, side.groups = _lib.MKV_ADDR_FLAT, 1, 1
+    spans = np.zeros(9, dtype=_lib.SPAN_DTYPE)
+    spans["n_tokens"] = 2
+    d.spans = spans.ctypes.data
+    d.n_spans, d.total_tokens = 9, 18
+    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
+    d.n_spans = 2
+    d.total_tokens = 3  # the spans hold 4
+    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    assert b"total_tokens" in lib.mkv_last_error()
+    spans["n_tokens"][0] = -1
+    d.total_tokens = 4
+    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    spans["n_tokens"][0] = 2
+    idx = np.zeros(65, np.int64)
+    d.dst.mode, d.dst.block_size, d.dst.index, d.dst.index_len = (
+        _lib.MKV_ADDR_SLOTS, 16, idx.ctypes.data, 65)
+    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
+    d.dst.index_len = 4
+    d.heads = 2  # 2 of the 4 rows a bf16 wave covers: not the direct geometry
+    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
+    d.heads, d.dst.block_size = 8, 24
+    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
 
 
 def test_python_api_refuses_tensors_off_the_gpu():

@@ -134,31 +134,40 @@ def _build(c, gpu):
                       1 if c["src_layout"] == "flat" else bs)
     dst_cs = CacheSet([[t.to(gpu) for t in row] for row in dst_caches], c["dst_layout"],
                       1 if c["dst_layout"] == "flat" else bs)
-    plan = ShiftPlan(spans, src_cs, dst_cs, inv_freq=inv,
-                     src_mode="flat" if c["src_layout"] == "flat" else "table",
-                     src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
-                     k_scale=k_scale)
+    plans = [ShiftPlan(spans, src_cs, dst_cs, inv_freq=inv,
+                       src_mode="flat" if c["src_layout"] == "flat" else "table",
+                       src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
+                       k_scale=k_scale, direct=direct) for direct in (False, True)]
     src_o = oracle_side(src_cs, "flat" if c["src_layout"] == "flat" else "table", src_index)
     dst_o = oracle_side(dst_cs, c["dst_mode"], dst_index)
-    return plan, dst_cs, spans, src_o, dst_o, inv, k_scale
+    return plans, dst_cs, spans, src_o, dst_o, inv, k_scale
 
 
 @pytest.mark.parametrize("seed", range(max(48, _EXTRA)))
 def test_random_batched_shift_matches_oracle(gpu, seed):
+    """Each case runs twice from the same starting caches: the two-launch path (plan
+    pass and workspace) and the direct single-launch path, where the case is eligible
+    for it (up to 63 spans, power-of-two blocks, heads a multiple of a wave's rows)."""
     c = _case(seed)
     desc = {k: (str(v) if k == "dtype" else v) for k, v in c.items() if k != "rng"}
     print(f"case random {desc}", flush=True)
-    plan, dst_cs, spans, src_o, dst_o, inv, k_scale = _build(c, gpu)
+    plans, dst_cs, spans, src_o, dst_o, inv, k_scale = _build(c, gpu)
     inv_np = np.zeros(0, np.float32) if inv is None else inv.numpy()
     orc.shift_spans(oracle_spans(spans), src_o, dst_o, inv_np, dname(c["dtype"]),
                     None if k_scale is None else k_scale.numpy())
-    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
-    plan.launch(error_flags=flags)
-    torch.cuda.synchronize(gpu)
-    assert int(flags.item()) == 0
-    for g, row in enumerate(dst_cs.caches):
-        for layer, t in enumerate(row):
-            assert np.array_equal(bits(t), dst_o.caches[g][layer]), f"group {g} layer {layer}"
+    start = [[t.clone() for t in row] for row in dst_cs.caches]
+    for plan in plans:
+        for row, row0 in zip(dst_cs.caches, start):
+            for t, t0 in zip(row, row0):
+                t.copy_(t0)
+        flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+        plan.launch(error_flags=flags)
+        torch.cuda.synchronize(gpu)
+        assert int(flags.item()) == 0, plan.direct
+        for g, row in enumerate(dst_cs.caches):
+            for layer, t in enumerate(row):
+                assert np.array_equal(bits(t), dst_o.caches[g][layer]), (
+                    f"group {g} layer {layer} direct={plan.direct}")
 
 
 @pytest.mark.parametrize("seed", range(max(24, _EXTRA // 2)))

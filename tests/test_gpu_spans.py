@@ -363,12 +363,14 @@ def test_single_span_out_of_range_slot_is_flagged_and_skipped(gpu, heads):
     assert torch.equal(kv.view(torch.int16), kv_ok.view(torch.int16))
 
 
-def test_plan_launched_on_another_stream(gpu):
+@pytest.mark.parametrize("direct", [False, True])
+def test_plan_launched_on_another_stream(gpu, direct):
     """A plan built on the current stream (its tables copied there) and launched at once
-    on a side stream, with no host synchronisation in between: the launch waits for the
-    copy's event and keeps the plan's buffers alive on that stream.  Every destination
-    byte against the oracle, then a second launch on the same side stream."""
-    print("case plan launched on a side stream", flush=True)
+    on a side stream, with no host synchronisation in between: the launch first makes
+    the side stream wait for the build stream and for the caches' base-address tables,
+    and keeps the plan's buffers alive on that stream.  Every destination byte against
+    the oracle, then a second launch on the same side stream."""
+    print(f"case plan launched on a side stream direct={direct}", flush=True)
     wl = W.qwen3_14b_multispan(gpu, layers=2, history=1024, dst_fill="random")
     src_o = oracle_side(wl.src, wl.src_mode, wl.src_index)
     dst_o = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
@@ -378,9 +380,10 @@ def test_plan_launched_on_another_stream(gpu):
     flags = torch.zeros(1, dtype=torch.int32, device=gpu)
     torch.cuda.synchronize(gpu)
     # the caches and flags are complete (synchronised above); the plan's tables are
-    # copied on the current stream, and only the plan's own event orders that copy
+    # copied on the current stream, and only the launch's stream wait orders that copy
     # before the side-stream launch
-    plan = wl.plan()
+    plan = wl.plan(direct=direct)
+    assert plan.direct is direct
     plan.launch(side.cuda_stream, error_flags=flags)
     plan.launch(side.cuda_stream, error_flags=flags)  # a second launch: same bytes
     side.synchronize()
@@ -389,13 +392,16 @@ def test_plan_launched_on_another_stream(gpu):
         assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
 
 
-def test_plan_launch_replays_from_a_hip_graph(gpu):
+@pytest.mark.parametrize("direct", [False, True])
+def test_plan_launch_replays_from_a_hip_graph(gpu, direct):
     """A captured launch replays exactly like an eager one: three replays, with eager
     work between them (new source values, a cleared destination, an eager launch that
-    gives the expected bytes), each replay checked byte for byte."""
-    print("case graph capture of a batched plan", flush=True)
+    gives the expected bytes), each replay checked byte for byte.  Both kernel paths:
+    plan pass + shift, and the direct single launch."""
+    print(f"case graph capture of a batched plan direct={direct}", flush=True)
     wl = W.qwen3_14b_multispan(gpu, layers=2, history=1024, dst_fill="zeros")
-    plan = wl.plan()
+    plan = wl.plan(direct=direct)
+    assert plan.direct is direct
     flags = torch.zeros(1, dtype=torch.int32, device=gpu)
     plan.launch(error_flags=flags)  # warm-up, eager
     torch.cuda.synchronize(gpu)
@@ -546,3 +552,45 @@ def test_more_spans_than_one_launch_takes(gpu):
     assert int(flags.item()) == 0
     for layer in range(layers):
         assert np.array_equal(bits(kv[layer]), dst_o.caches[0][layer]), f"layer {layer}"
+
+
+def test_direct_path_flags_a_prefix_that_disagrees_with_the_spans(gpu):
+    """The direct path trusts no caller prefix: a prefix whose steps differ from the
+    spans' token counts raises MKV_FLAG_SPAN, and the tokens it does map still land on
+    their own rows (every row bounds-checked), so nothing outside the spans' rows is
+    written."""
+    import ctypes
+
+    from marathon_amd import _lib
+    from marathon_amd.shift_kernels import current_stream
+
+    print("case direct path with a bad prefix", flush=True)
+    wl = W.qwen3_14b_multispan(gpu, layers=2, history=1024, dst_fill="random")
+    plan = wl.plan(direct=True)
+    assert plan.direct
+    counts = [int(c) for c in wl.spans["n_tokens"]]
+    good = np.concatenate(([0], np.cumsum(counts))).astype(np.int64)
+    bad = good.copy()
+    bad[1] -= 5  # span 0's last 5 tokens are never mapped; span 1 starts 5 early
+    dst_o = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
+    src_o = oracle_side(wl.src, wl.src_mode, wl.src_index)
+    torch.cuda.synchronize(gpu)
+    before = [bits(t) for t in wl.dst.caches[0]]
+    orc.shift_spans(oracle_spans(wl.spans), src_o, dst_o, wl.inv_freq.numpy(), "bf16")
+    starts = torch.from_numpy(bad).to(gpu)
+    d = plan.descs[0]
+    d.span_starts = starts.data_ptr()
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    d.error_flags = flags.data_ptr()
+    _lib.check(_lib.lib().mkv_shift_spans(ctypes.byref(d), ctypes.c_void_p(current_stream(gpu))))
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) & _lib.MKV_FLAG_SPAN
+    # every destination row is either untouched or the oracle's (no stray writes)
+    for layer, t in enumerate(wl.dst.caches[0]):
+        def tokens(a):  # HND [blocks, heads, 16, 2D] -> one row per (block, offset)
+            return a.transpose(0, 2, 1, 3)
+
+        got = tokens(bits(t))
+        ok = (got == tokens(before[layer])).all(axis=(-1, -2)) | (
+            got == tokens(dst_o.caches[0][layer])).all(axis=(-1, -2))
+        assert bool(ok.all()), f"layer {layer}: a row is neither untouched nor the oracle's"

@@ -254,15 +254,20 @@ def test_layout_detection(shape, hnd):  # vllm_shift_connector.py:396-402
 
 
 def test_paged_index_tables_and_slots():
-    """Device-side slots: block tables concatenated with per-item offsets; a batch with
+    """Device-side slots: each item's window of its block table (the blocks its positions
+    touch), concatenated, with per-item (position in the window, offset); a batch with
     any host slots falls back to concatenated int64 slots (from_blocks items expanded)."""
     from marathon_amd.connector import Load, Save, paged_index
 
     a = Load.from_blocks("s", [7, 3, 9], 5, 40, -2)
     b = Load.from_blocks("t", [1, 2], 16, 32, 4)
     mode, index, rows = paged_index([a, b], 16)
-    assert mode == "table" and index.tolist() == [7, 3, 9, 1, 2]
-    assert rows == [(5, 0), (16, 3)]
+    assert mode == "table" and index.tolist() == [7, 3, 9, 2]
+    assert rows == [(5, 0), (0, 3)]
+    # the windows resolve to the same slots as the whole tables
+    for it, (pos, off) in zip((a, b), rows):
+        got = [index[off + (pos + i) // 16].item() * 16 + (pos + i) % 16 for i in range(it.n)]
+        assert got == slots(it.block_ids, it.paged_pos, it.paged_pos + it.n, 16).tolist()
     assert (a.src_start, a.n, b.src_start, b.n) == (7, 35, 12, 16)
     c = Load("u", slots([4], 0, 3, 16), 0, 0)
     mode, index, rows = paged_index([a, c], 16)
