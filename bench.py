@@ -31,6 +31,9 @@ Prints one JSON line.  Also measured, in the same line:
   block tables made the identity: what the GPU streams with nothing scattered.
 * ``dst_layouts``: the headline shift into fused NHD caches and into caches that keep K
   and V in separate planes, beside the fused HND headline.
+* ``connector_step`` / ``save_step``: the connector's load and save calls end to end.
+* ``plan_variants``: A/B of the token records' order (span order against destination
+  page order) and of the single-launch direct path against the two-launch path.
 """
 
 from __future__ import annotations
@@ -593,6 +596,117 @@ def dst_layouts(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def _same_output(a_plan, b_plan, caches) -> bool:
+    """Run two plans of one workload into zeroed caches; whether every byte matches."""
+    import torch
+
+    for c in caches:
+        c.zero_()
+    a_plan.launch()
+    torch.cuda.synchronize()
+    first = [c.clone() for c in caches]
+    for c in caches:
+        c.zero_()
+    b_plan.launch()
+    torch.cuda.synchronize()
+    return all(torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+               for x, y in zip(first, caches))
+
+
+def _ab(plans: dict, steps: int, warmup: int, stream, rounds: int = 3) -> dict:
+    """Median launch time of each plan (HIP events), each plan's launches back to back,
+    the plans alternating over ``rounds``; the best round's median per plan."""
+    import numpy as np
+
+    best = {name: float("inf") for name in plans}
+    for _ in range(rounds):
+        for name, plan in plans.items():
+            _, per = time_plan(plan, steps, warmup, stream)
+            best[name] = min(best[name], float(np.median(per)))
+    return best
+
+
+def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
+    """A/B of the plan options, each pair on one workload with byte-identical output.
+
+    * ``record_order``: the two-launch path's token records in span order (the default)
+      against ``order="dst_page"`` (records sorted by the 2 MB page of the destination
+      row, which costs an ordered plan pass and two more small launches), on the fp8 and
+      bf16 Qwen3-14B multi-span shifts and one GPU's fp8 share at 1 KV head.
+    * ``direct``: the single-launch path (token prefix and rotation tables from the
+      host, no plan pass or workspace) against the two-launch path, for one span of
+      16 to 2,048 tokens x 40 layers (flat store -> HND paged cache through shuffled
+      slots, delta 186).  ``ShiftPlan`` takes the direct path by default up to
+      ``DIRECT_MAX_TOKEN_LAYERS`` token-layers.
+    """
+    import torch
+
+    from marathon_amd import spans as S
+    from marathon_amd import workloads as W
+    from marathon_amd.shift_kernels import inv_freq_for
+
+    out = {"record_order": {}, "direct": {"default_max_token_layers":
+                                          S.DIRECT_MAX_TOKEN_LAYERS}}
+    for name, make in (("qwen3_14b_multispan_fp8", lambda: W.qwen3_14b_multispan_fp8(dev)),
+                       ("qwen3_14b_multispan_bf16", lambda: W.qwen3_14b_multispan(dev)),
+                       ("qwen3_14b_multispan_fp8_1_head",
+                        lambda: W.qwen3_14b_multispan_fp8(dev, heads=1))):
+        log(f"record order A/B: {name}")
+        wl = make()
+        plans = {"none": wl.plan(direct=False, order="none"),
+                 "dst_page": wl.plan(direct=False, order="dst_page")}
+        same = _same_output(plans["none"], plans["dst_page"], wl.dst.caches[0])
+        warm_up(lambda: plans["none"].launch(stream.cuda_stream))
+        ms = _ab(plans, max(steps, 30), warmup, stream)
+        gb = plans["none"].algorithmic_bytes
+        out["record_order"][name] = {
+            **{f"{k}_ms": round(v, 4) for k, v in ms.items()},
+            **{f"{k}_frac_of_peak": round(gb / (v / 1e3) / 1e9 / PEAK_GBS, 4)
+               for k, v in ms.items()},
+            "dst_page_gain_pct": round(100 * (ms["none"] / ms["dst_page"] - 1), 2),
+            "bit_identical": same,
+        }
+        del wl, plans
+        torch.cuda.empty_cache()
+
+    layers, heads, d, bs = 40, 8, 128, 16
+    for n in (16, 64, 256, 512, 2048):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(n)
+        blocks = -(-n // bs) + 8
+        src = [torch.randn(n, heads, 2 * d, dtype=torch.bfloat16, device=dev, generator=gen)
+               for _ in range(layers)]
+        kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
+              for _ in range(layers)]
+        table = torch.randperm(blocks, device=dev, generator=gen)
+        pos = torch.arange(n, device=dev)
+        slot = table[pos // bs] * bs + pos % bs
+        src_set, dst_set = S.CacheSet([src], "flat"), S.CacheSet([kv], "hnd", bs)
+
+        def make(direct):
+            return S.ShiftPlan(S.span_array([(0, 0, 0, 0, n, 186, 0, 0)]), src_set, dst_set,
+                               inv_freq=inv_freq_for(d, 1e6), src_mode="flat",
+                               dst_mode="slots", dst_index=slot, direct=direct)
+
+        plans = {"direct": make(True), "two_launch": make(False)}
+        if not plans["direct"].direct:
+            raise AssertionError("the direct path refused an eligible shift")
+        same = _same_output(plans["direct"], plans["two_launch"], kv)
+        warm_up(lambda: plans["direct"].launch(stream.cuda_stream))
+        ms = _ab(plans, max(steps, 50), warmup, stream)
+        gb = plans["direct"].algorithmic_bytes
+        out["direct"][f"tokens_{n}"] = {
+            "token_layers": n * layers,
+            **{f"{k}_ms": round(v, 4) for k, v in ms.items()},
+            **{f"{k}_frac_of_peak": round(gb / (v / 1e3) / 1e9 / PEAK_GBS, 4)
+               for k, v in ms.items()},
+            "bit_identical": same,
+        }
+        del src, kv, plans, src_set, dst_set
+        torch.cuda.empty_cache()
+    return out
+
+
 def connector_step(dev, steps: int, warmup: int) -> dict:
     """Worker load steps through the connector: a session held in the block-layout store,
     loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
@@ -767,9 +881,24 @@ def main() -> int:
                     help="skip the headline shift into the other paged-cache layouts")
     ap.add_argument("--no-connector-step", action="store_true",
                     help="skip the end-to-end connector load and save step timings")
+    ap.add_argument("--no-plan-variants", action="store_true",
+                    help="skip the A/B of record order and of the direct path")
+    ap.add_argument("--only", default="",
+                    help="comma-separated informational sections to run (e.g. "
+                    "'plan_variants'); every other one, the CPU baseline included, is "
+                    "skipped")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (for PMC counter scaling)")
     args = ap.parse_args()
+    if args.only:
+        keep = {x.strip() for x in args.only.split(",") if x.strip()}
+        sections = {"reference_shape", "reference_loop", "other_workloads", "tp_shares",
+                    "size_sweep", "ceilings", "dst_layouts", "connector_step",
+                    "plan_variants", "cpu_baseline"}
+        if keep - sections:
+            ap.error(f"--only: unknown sections {sorted(keep - sections)}")
+        for name in sections - keep:
+            setattr(args, "no_" + name, True)
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: the shift needs no collective and this library runs on "
@@ -847,10 +976,13 @@ def main() -> int:
         extra["connector_step"] = connector_step(dev, side_steps, args.warmup)
         log("connector save step (paged -> block store)")
         extra["save_step"] = save_step(dev, side_steps, args.warmup)
-    log("Qwen3-0.6B shift on the HIP path (the CPU baseline's small case)")
-    small = qwen3_0_6b_hip(dev, side_steps, args.warmup, stream)
-    cpu = None
+    if not args.no_plan_variants:
+        log("plan variants: record order and direct path A/B")
+        extra["plan_variants"] = plan_variants(dev, side_steps, args.warmup, stream)
+    small = cpu = None
     if not args.no_cpu_baseline:
+        log("Qwen3-0.6B shift on the HIP path (the CPU baseline's small case)")
+        small = qwen3_0_6b_hip(dev, side_steps, args.warmup, stream)
         log("cpu baseline (reference torch path on the host, the Qwen3-14B multi-span shift)")
         cpu = cpu_baseline(gpu_small=small)
 

@@ -77,6 +77,11 @@ extern "C" {
 #define MKV_ADDR_TABLE 2 /* slot = tbl[span.*_index + pos / bs] * bs + pos % bs,
                             tbl = (const int32_t*)index, pos = span.*_pos + i */
 
+/* Token orders of the batched entry point (mkv_shift_desc_t.order). */
+#define MKV_ORDER_NONE 0
+#define MKV_ORDER_DST_PAGE 1
+#define MKV_ORDER_EXTRA_BYTES(total_tokens) ((int64_t)(total_tokens) * 32 + (1 << 20))
+
 /* Limits of the batched entry point. */
 #define MKV_MAX_SPANS 4096
 #define MKV_MAX_HEAD_SIZE 512
@@ -163,6 +168,13 @@ typedef struct mkv_side {
  *                  ignored, and the two-launch path with its workspace runs.  A prefix
  *                  that disagrees with the spans raises MKV_FLAG_SPAN; its tokens are
  *                  bounds-checked like any other.
+ *   order        : MKV_ORDER_NONE, or MKV_ORDER_DST_PAGE: on the two-launch path, the
+ *                  resolved tokens are sorted by the 2 MB page of their destination row
+ *                  before the shift (a stable sort: the tokens of one page keep their
+ *                  order; two more small launches), so that the workgroups running
+ *                  together touch few destination pages.  The workspace then needs
+ *                  MKV_ORDER_EXTRA_BYTES(total_tokens) more bytes.  Results are the same
+ *                  bytes either way.  Ignored on the direct path.
  */
 typedef struct mkv_shift_desc {
   const mkv_span_t* spans;
@@ -182,6 +194,8 @@ typedef struct mkv_shift_desc {
   mkv_side_t dst;
   const int64_t* span_starts;
   const float* span_tables;
+  int32_t order;
+  int32_t reserved;
 } mkv_shift_desc_t;
 
 /*
@@ -270,7 +284,7 @@ const char* mkv_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. */
 int32_t mkv_abi_version(void);
-#define MKV_ABI_VERSION ((3 << 16) | 1)
+#define MKV_ABI_VERSION ((3 << 16) | 2)
 
 #ifdef __cplusplus
 }

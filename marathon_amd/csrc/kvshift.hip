@@ -175,6 +175,8 @@ struct PlanParams {
   const float* inv_freq;
   float* tables;  // [n_spans][2][rotary]: cos by element, then sgn by element
   TokRec* recs;   // [total_tokens]
+  uint32_t* order_hist;  // ordered: [gridDim.x][kOrderBuckets] page counts per workgroup
+  int64_t order_chunk;   // ordered: tokens per workgroup (contiguous)
   int32_t* err;
   int64_t total_tokens;
   int32_t n_spans;
@@ -496,6 +498,17 @@ __device__ __forceinline__ int span_of(const int64_t* starts, int n_spans, int64
   return static_cast<int>(__popcll(__ballot(v <= g))) - 1;
 }
 
+// Destination-page order (MKV_ORDER_DST_PAGE): a record's bucket is the 2 MB page of its
+// destination row; pages past the last bucket share it.
+constexpr int kOrderBuckets = 1024;
+constexpr int kOrderMaxGroups = 256;  // workgroups of an ordered plan pass (and scatter)
+
+__device__ __forceinline__ uint32_t order_bucket(const TokRec& r) {
+  if (r.span < 0) return 0;
+  const uint64_t page = static_cast<uint64_t>(r.dst_off) >> 21;
+  return page < kOrderBuckets ? static_cast<uint32_t>(page) : kOrderBuckets - 1;
+}
+
 // This lane's C cos / signed-sin values of a span's rotation, computed as the plan pass
 // computes its tables (fp32 angle, double-precision sincos, rounded to fp32).
 template <int C>
@@ -578,8 +591,20 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
     t[p.rotary + f + half] = sn;
   }
 
-  // token records
-  for (int64_t g = gtid; g < p.total_tokens; g += gstride) {
+  // token records: grid-stride, or (ordered) one contiguous chunk per workgroup with
+  // its page histogram
+  __shared__ uint32_t s_hist[kOrderBuckets];
+  const bool ordered = p.order_hist != nullptr;
+  int64_t g_lo = gtid, g_hi = p.total_tokens, g_step = gstride;
+  if (ordered) {
+    for (int b = tid; b < kOrderBuckets; b += kPlanThreads) s_hist[b] = 0;
+    __syncthreads();
+    g_lo = static_cast<int64_t>(blockIdx.x) * p.order_chunk;
+    g_hi = min(g_lo + p.order_chunk, p.total_tokens);
+    g_lo += tid;
+    g_step = kPlanThreads;
+  }
+  for (int64_t g = g_lo; g < g_hi; g += g_step) {
     TokRec r;
     r.src_off = 0;
     r.dst_off = 0;
@@ -620,6 +645,93 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
       }
     }
     p.recs[g] = r;
+    if (ordered) atomicAdd(&s_hist[order_bucket(r)], 1u);
+  }
+  if (ordered) {
+    __syncthreads();
+    for (int b = tid; b < kOrderBuckets; b += kPlanThreads)
+      p.order_hist[static_cast<int64_t>(blockIdx.x) * kOrderBuckets + b] = s_hist[b];
+  }
+}
+
+// -------------------------------------------------------------------- order kernels
+//
+// Optional (MKV_ORDER_DST_PAGE): the plan's records, sorted stably by the 2 MB page of
+// their destination row, so that the workgroups running together touch few destination
+// pages while the tokens of one destination block stay together and in order (each
+// record still carries its span, so the per-span tables are unchanged).  Three steps:
+// the ordered plan pass resolves one contiguous chunk of tokens per workgroup and counts
+// its pages; order_scan_kernel turns the counts, bucket-major, into each (page,
+// workgroup)'s first output position; order_scatter_kernel writes every chunk's records
+// there in token order (ranks within a wave from ballots, waves and batches in order).
+
+constexpr int kScanThreads = kOrderBuckets;  // one thread per page bucket
+
+// hist: [groups][kOrderBuckets] page counts of each workgroup's chunk, rewritten as each
+// (workgroup, page)'s first output position, pages major: thread b walks bucket b down
+// the workgroups (coalesced across threads), then the buckets' totals are scanned.
+__global__ __launch_bounds__(kScanThreads) void order_scan_kernel(uint32_t* hist, int groups) {
+  __shared__ uint32_t part[kScanThreads];
+  const int b = threadIdx.x;
+  uint32_t total = 0;
+  for (int w = 0; w < groups; ++w) total += hist[static_cast<int64_t>(w) * kOrderBuckets + b];
+  part[b] = total;
+  __syncthreads();
+  for (int off = 1; off < kScanThreads; off <<= 1) {
+    const uint32_t v = b >= off ? part[b - off] : 0u;
+    __syncthreads();
+    part[b] += v;
+    __syncthreads();
+  }
+  uint32_t run = part[b] - total;
+  for (int w = 0; w < groups; ++w) {
+    uint32_t* h = hist + static_cast<int64_t>(w) * kOrderBuckets + b;
+    const uint32_t c = *h;
+    *h = run;
+    run += c;
+  }
+}
+
+constexpr int kScatterThreads = 256;
+
+__global__ __launch_bounds__(kScatterThreads) void order_scatter_kernel(
+    const TokRec* in, TokRec* out, const uint32_t* offsets, int64_t total, int64_t chunk) {
+  __shared__ uint32_t running[kOrderBuckets];  // records of each page placed so far
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int b = tid; b < kOrderBuckets; b += kScatterThreads) running[b] = 0;
+  const int64_t lo = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t hi = min(lo + chunk, total);
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  for (int64_t b0 = lo; b0 < hi; b0 += kScatterThreads) {
+    const int64_t g = b0 + tid;
+    const bool valid = g < hi;
+    TokRec r{};
+    if (valid) r = in[g];
+    const uint32_t key = valid ? order_bucket(r) : 0u;
+    uint32_t pos = 0;
+    __syncthreads();  // the previous batch's updates of `running` are done
+    for (int w = 0; w < kScatterThreads / 64; ++w) {
+      if (wave == w) {
+        // the distinct pages of this wave, one ballot each, in lane order
+        uint64_t todo = __ballot(valid);
+        while (todo != 0) {
+          const int leader = __ffsll(static_cast<long long>(todo)) - 1;
+          const uint32_t k = static_cast<uint32_t>(
+              __builtin_amdgcn_readlane(static_cast<int>(key), leader));
+          const uint64_t same = __ballot(valid && key == k);
+          const uint32_t base = running[k];
+          if (valid && key == k)
+            pos = offsets[static_cast<int64_t>(blockIdx.x) * kOrderBuckets + k] + base +
+                  static_cast<uint32_t>(__popcll(same & below));
+          if (lane == leader) running[k] = base + static_cast<uint32_t>(__popcll(same));
+          todo &= ~same;
+        }
+      }
+      __syncthreads();
+    }
+    if (valid) out[pos] = r;
   }
 }
 
@@ -1319,7 +1431,11 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
     return launch_any<true>(d->dtype, true, true, sp, tiles, d->layers, st);
   }
 
-  const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary);
+  if (d->order != MKV_ORDER_NONE && d->order != MKV_ORDER_DST_PAGE)
+    return fail(MKV_ERR_ARG, "unknown order %d", d->order);
+  const bool ordered = d->order == MKV_ORDER_DST_PAGE;
+  const int64_t need = workspace_bytes(d->total_tokens, d->n_spans, d->rotary) +
+                       (ordered ? MKV_ORDER_EXTRA_BYTES(d->total_tokens) : 0);
   void* ws_ptr = d->workspace;
   int64_t ws_bytes = d->workspace_bytes;
   if (noalloc) {
@@ -1365,11 +1481,34 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   int64_t plan_grid = (work + kPlanThreads - 1) / kPlanThreads;
   if (plan_grid > 4096) plan_grid = 4096;
   if (plan_grid < 1) plan_grid = 1;
+  TokRec* sorted = nullptr;
+  if (ordered) {  // sorted records, then the page counts, after the plan's records
+    int64_t groups = (d->total_tokens + kPlanThreads - 1) / kPlanThreads;
+    if (groups > kOrderMaxGroups) groups = kOrderMaxGroups;
+    if (groups < 1) groups = 1;
+    plan_grid = groups;
+    pp.order_chunk = (d->total_tokens + groups - 1) / groups;
+    sorted = recs + d->total_tokens;
+    pp.order_hist = reinterpret_cast<uint32_t*>(sorted + d->total_tokens);
+  }
   const size_t lds = sizeof(int64_t) * (static_cast<size_t>(d->n_spans) + 1);
   hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kPlanThreads), lds,
                      st, pp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "plan launch failed: %s", hipGetErrorString(e));
+  if (ordered) {
+    hipLaunchKernelGGL(order_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, pp.order_hist,
+                       static_cast<int>(plan_grid));
+    e = hipGetLastError();
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(order_scatter_kernel, dim3(static_cast<unsigned>(plan_grid)),
+                         dim3(kScatterThreads), 0, st, recs, sorted, pp.order_hist,
+                         d->total_tokens, pp.order_chunk);
+      e = hipGetLastError();
+    }
+    if (e != hipSuccess) return fail(MKV_ERR_HIP, "order launch failed: %s", hipGetErrorString(e));
+    recs = sorted;
+  }
 
   sp.recs = recs;
   sp.tables = tables;

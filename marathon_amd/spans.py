@@ -37,6 +37,12 @@ MODES = {"flat": _lib.MKV_ADDR_FLAT, "slots": _lib.MKV_ADDR_SLOTS, "table": _lib
 DIRECT_MAX_TOKEN_LAYERS = 4096
 
 
+#: Token orders of the two-launch path (``mkv_shift_desc_t.order``).
+ORDERS = {"none": _lib.MKV_ORDER_NONE, "dst_page": _lib.MKV_ORDER_DST_PAGE}
+#: The order each element type takes by default (see ``ShiftPlan(order=...)``).
+DEFAULT_ORDER: dict = {}
+
+
 class _on:
     """``torch.cuda.device(device)`` only when ``device`` is not already current."""
 
@@ -224,6 +230,10 @@ class ShiftPlan:
     :meth:`direct_eligible` allows it, with the token prefix and the per-span rotation
     tables computed here (:func:`span_tables`); False always runs the two-launch path
     (plan pass and workspace), True asks for the direct path where eligible.
+
+    ``order``: the order the two-launch path moves tokens in -- ``"none"`` (span order)
+    or ``"dst_page"`` (sorted by the 2 MB page of each token's destination row, one
+    more small launch); None takes :data:`DEFAULT_ORDER` for the element type.
     """
 
     def __init__(
@@ -239,6 +249,7 @@ class ShiftPlan:
         dst_index: torch.Tensor | None = None,
         k_scale: torch.Tensor | None = None,
         direct: bool | None = None,
+        order: str | None = None,
     ):
         spans = np.ascontiguousarray(np.asarray(spans, dtype=_lib.SPAN_DTYPE))
         if src.layers != dst.layers:
@@ -328,10 +339,17 @@ class ShiftPlan:
         step = _lib.MKV_MAX_SPANS
         chunks = [(lo, min(step, self.n_spans - lo)) for lo in range(0, self.n_spans, step)]
         self.workspace = None
+        if order is None:
+            order = DEFAULT_ORDER.get(self.dtype, "none")
+        if order not in ORDERS:
+            raise ValueError(f"order {order!r}: one of {sorted(ORDERS)}")
+        self.order = "none" if self.direct else order
         if not self.direct:
             L = _lib.lib()
+            ordered = self.order != "none"  # sorted records and page counts
             need = max(
                 (L.mkv_shift_workspace_size(sum(counts[lo:lo + cnt]), cnt, self.rotary)
+                 + (32 * sum(counts[lo:lo + cnt]) + (1 << 20) if ordered else 0)
                  for lo, cnt in chunks),
                 default=0,
             )
@@ -347,6 +365,7 @@ class ShiftPlan:
             else:
                 d.workspace = self.workspace.data_ptr()
                 d.workspace_bytes = self.workspace.numel()
+                d.order = ORDERS[self.order]
             d.total_tokens = sum(counts[lo:lo + cnt])
             d.inv_freq = ptr(inv)
             d.k_scale = ptr(scale)

@@ -147,7 +147,7 @@ class Workload:
     v_scale: torch.Tensor | None = None
     meta: dict = field(default_factory=dict)
 
-    def plan(self, direct: bool | None = None) -> ShiftPlan:
+    def plan(self, direct: bool | None = None, order: str | None = None) -> ShiftPlan:
         return ShiftPlan(
             self.spans,
             self.src,
@@ -159,6 +159,7 @@ class Workload:
             dst_index=self.dst_index,
             k_scale=self.k_scale,
             direct=direct,
+            order=order,
         )
 
     @property

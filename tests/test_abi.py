@@ -62,6 +62,7 @@ int main(void) {
   O(mkv_shift_desc_t, heads); O(mkv_shift_desc_t, head_size); O(mkv_shift_desc_t, rotary);
   O(mkv_shift_desc_t, dtype); O(mkv_shift_desc_t, src); O(mkv_shift_desc_t, dst);
   O(mkv_shift_desc_t, span_starts); O(mkv_shift_desc_t, span_tables);
+  O(mkv_shift_desc_t, order);
   return 0;
 }
 """

@@ -137,7 +137,8 @@ def _build(c, gpu):
     plans = [ShiftPlan(spans, src_cs, dst_cs, inv_freq=inv,
                        src_mode="flat" if c["src_layout"] == "flat" else "table",
                        src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
-                       k_scale=k_scale, direct=direct) for direct in (False, True)]
+                       k_scale=k_scale, direct=direct, order=order)
+             for direct, order in ((False, "none"), (False, "dst_page"), (True, None))]
     src_o = oracle_side(src_cs, "flat" if c["src_layout"] == "flat" else "table", src_index)
     dst_o = oracle_side(dst_cs, c["dst_mode"], dst_index)
     return plans, dst_cs, spans, src_o, dst_o, inv, k_scale
@@ -145,9 +146,10 @@ def _build(c, gpu):
 
 @pytest.mark.parametrize("seed", range(max(48, _EXTRA)))
 def test_random_batched_shift_matches_oracle(gpu, seed):
-    """Each case runs twice from the same starting caches: the two-launch path (plan
-    pass and workspace) and the direct single-launch path, where the case is eligible
-    for it (up to 63 spans, power-of-two blocks, heads a multiple of a wave's rows)."""
+    """Each case runs three times from the same starting caches: the two-launch path
+    (plan pass and workspace) in span order and in destination-page order, and the
+    direct single-launch path, where the case is eligible for it (up to 63 spans,
+    power-of-two blocks, heads a multiple of a wave's rows)."""
     c = _case(seed)
     desc = {k: (str(v) if k == "dtype" else v) for k, v in c.items() if k != "rng"}
     print(f"case random {desc}", flush=True)
@@ -167,7 +169,7 @@ def test_random_batched_shift_matches_oracle(gpu, seed):
         for g, row in enumerate(dst_cs.caches):
             for layer, t in enumerate(row):
                 assert np.array_equal(bits(t), dst_o.caches[g][layer]), (
-                    f"group {g} layer {layer} direct={plan.direct}")
+                    f"group {g} layer {layer} direct={plan.direct} order={plan.order}")
 
 
 @pytest.mark.parametrize("seed", range(max(24, _EXTRA // 2)))
