@@ -88,6 +88,14 @@
 #ifndef MKV_STORE_CPOL
 #define MKV_STORE_CPOL 18
 #endif
+// Layers one workgroup of the batched kernels moves (grid.y = ceil(layers / this)): the
+// token metadata of a pass is resolved once for all of them.  Direct path, record path.
+#ifndef MKV_LAYERS_DIRECT
+#define MKV_LAYERS_DIRECT 1
+#endif
+#ifndef MKV_LAYERS_RECORDS
+#define MKV_LAYERS_RECORDS 1
+#endif
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs; with
 // the remap, XCD k walks the k-th contiguous eighth of the tiles (smaller per-XCD set
 // of pages in flight).  0 = plain order.
@@ -99,6 +107,11 @@ namespace {
 
 constexpr int kThreads = MKV_WG_THREADS;  // shift kernel; a multiple of the 64-lane wave
 constexpr int kWaves = kThreads / 64;
+
+template <bool BATCHED, bool DIRECT>
+constexpr int layer_batch() {
+  return !BATCHED ? 1 : DIRECT ? MKV_LAYERS_DIRECT : MKV_LAYERS_RECORDS;
+}
 constexpr int kPlanThreads = 256;  // plan kernel
 // Buffer resources for the stores: raw (stride 0), the whole 32-bit range checked by
 // the hardware (a lane's offset is below 2^31, checked on the host), and the gfx9
@@ -749,6 +762,8 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   using E = Elem<DT>;
   constexpr int C = E::kPerChunk;
   constexpr int U = E::kPasses;
+  constexpr int LB = layer_batch<BATCHED, DIRECT>();
+  constexpr int N = U * LB;  // (pass, layer) units of one sweep: x = u * LB + lb
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -764,7 +779,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   const int partner_addr = (partner & 63) * 4;
   const uint32_t chunk_off = static_cast<uint32_t>(j) * 16u;
   const int H = p.heads;
-  const int layer = blockIdx.y;
+  const int layer0 = blockIdx.y * LB;
 
   int64_t tile = blockIdx.x;
   if (MKV_XCDS > 1) {
@@ -798,11 +813,22 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   const uint32_t d_lane = UNIFORM ? static_cast<uint32_t>(row_in_wave) *
                                             static_cast<uint32_t>(p.dst_hstride) + chunk_off
                                   : chunk_off;
+  // the workgroup's layers; the last batch of a layer count that LB does not divide
+  // has layers past the end, which move nothing
+  bool lay_ok[LB];
+  int lay[LB];  // clamped: base-table and scale reads stay in range
+#pragma unroll
+  for (int lb = 0; lb < LB; ++lb) {
+    lay_ok[lb] = layer0 + lb < p.layers;
+    lay[lb] = lay_ok[lb] ? layer0 + lb : p.layers - 1;
+  }
 
-  float scale = 1.0f;
+  float scale[LB], rcp[LB];
   float cs[C], sg[C];
 #pragma unroll
   for (int e = 0; e < C; ++e) cs[e] = 1.0f, sg[e] = 0.0f;
+#pragma unroll
+  for (int lb = 0; lb < LB; ++lb) scale[lb] = 1.0f;
   int cur_span = -1;
   if constexpr (!BATCHED) {
     if (p.rotate && rot_lane) {
@@ -813,29 +839,30 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
       }
     }
     if constexpr (DT == MKV_FP8_E4M3) {
-      if (p.rotate) scale = ld_const(p.k_scale);
+      if (p.rotate) scale[0] = ld_const(p.k_scale);
     }
   } else {
     // the scale dequantises K for the rotation; with rotary 0 nothing is rotated and
     // k_scale may be NULL
     if constexpr (DT == MKV_FP8_E4M3) {
-      if (p.rotary > 0) scale = ld_const(p.k_scale + layer);
+      if (p.rotary > 0) {
+#pragma unroll
+        for (int lb = 0; lb < LB; ++lb) scale[lb] = ld_const(p.k_scale + lay[lb]);
+      }
     }
   }
-  const float rcp = 1.0f / scale;  // correctly rounded (fp8 requantisation)
+#pragma unroll
+  for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f / scale[lb];  // correctly rounded
 
   for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
     // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
     // metadata is fetched first, then all base addresses, so the workgroup pays two
-    // metadata round trips in total rather than two per pass.
+    // metadata round trips in total rather than two per pass; a token's metadata serves
+    // every layer of the workgroup.
     bool live[U];
     int span_u[U], delta_u[U], head_u[U];
     int64_t s_at[U], d_at[U];  // byte offsets of the pass's (first) row
-    const char* sbk[U];
-    const char* sbv[U];
-    char* dbk[U];
-    char* dbv[U];
-    int sb_u[U], db_u[U];
+    int sb_u[U], db_u[U];      // the (group, layer 0) rows of the base tables
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row0 = r0 + (wave + kWaves * u) * rpw;
@@ -889,20 +916,21 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         delta_u[u] = ld_const(&sp->delta);
         s_at[u] = so;
         d_at[u] = dof;
-        sb_u[u] = (ok ? sg : 0) * p.layers + layer;
-        db_u[u] = (ok ? dg : 0) * p.layers + layer;
+        sb_u[u] = (ok ? sg : 0) * p.layers;
+        db_u[u] = (ok ? dg : 0) * p.layers;
       } else if constexpr (BATCHED) {
         const TokRec* rp = p.recs + g;
         span_u[u] = UNIFORM ? ld_const(&rp->span) : rp->span;
         delta_u[u] = UNIFORM ? ld_const(&rp->delta) : rp->delta;
         s_at[u] = UNIFORM ? ld_const(&rp->src_off) : rp->src_off;
         d_at[u] = UNIFORM ? ld_const(&rp->dst_off) : rp->dst_off;
-        sb_u[u] = (UNIFORM ? ld_const(&rp->src_base) : rp->src_base) + layer;
-        db_u[u] = (UNIFORM ? ld_const(&rp->dst_base) : rp->dst_base) + layer;
+        sb_u[u] = UNIFORM ? ld_const(&rp->src_base) : rp->src_base;
+        db_u[u] = UNIFORM ? ld_const(&rp->dst_base) : rp->dst_base;
       } else {
         span_u[u] = 0;
         delta_u[u] = p.rotate;
         s_at[u] = g * p.src_tstride;
+        sb_u[u] = db_u[u] = 0;
         const int64_t slot = UNIFORM ? ld_const(p.slots + g) : p.slots[g];
         if (live[u] && (slot < 0 || slot >= p.dst.num_slots)) {
           if (p.err != nullptr && (!UNIFORM || lane == 0)) atomicOr(p.err, MKV_FLAG_DST_RANGE);
@@ -918,66 +946,76 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         }
         d_at[u] = blk * p.dst.bstride + off * p.dst.ostride;
       }
+      if constexpr (BATCHED) live[u] = live[u] && span_u[u] >= 0;
+      s_at[u] += head_u[u] * p.src_hstride;
+      d_at[u] += head_u[u] * p.dst_hstride;
     }
+
+    // ---- the base address of every (pass, layer) unit
+    bool xl[N];
+    const char* sbk[N];
+    const char* sbv[N];
+    char* dbk[N];
+    char* dbv[N];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int x = 0; x < N; ++x) {
+      const int u = x / LB, lb = x % LB;
+      xl[x] = live[u] && lay_ok[lb];
       if constexpr (BATCHED) {
-        const int sb = sb_u[u], db = db_u[u];
-        if (UNIFORM && u > 0 && sb == sb_u[0] && db == db_u[0]) {
-          // the usual case: every pass of the tile belongs to one (group, layer)
-          sbk[u] = sbk[0];
-          sbv[u] = sbv[0];
-          dbk[u] = dbk[0];
-          dbv[u] = dbv[0];
+        const int sb = sb_u[u] + lay[lb], db = db_u[u] + lay[lb];
+        if (UNIFORM && u > 0 && sb_u[u] == sb_u[0] && db_u[u] == db_u[0]) {
+          // the usual case: every pass of the tile belongs to one group
+          sbk[x] = sbk[lb];
+          sbv[x] = sbv[lb];
+          dbk[x] = dbk[lb];
+          dbv[x] = dbv[lb];
         } else if (UNIFORM) {
-          sbk[u] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb));
-          sbv[u] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb));
-          dbk[u] = reinterpret_cast<char*>(ld_const(p.dst_k_base + db));
-          dbv[u] = reinterpret_cast<char*>(ld_const(p.dst_v_base + db));
+          sbk[x] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb));
+          sbv[x] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb));
+          dbk[x] = reinterpret_cast<char*>(ld_const(p.dst_k_base + db));
+          dbv[x] = reinterpret_cast<char*>(ld_const(p.dst_v_base + db));
         } else {
           // rows of several tokens: they usually share one (group, layer) base row,
           // read with scalar loads (a per-lane gather measured 6-10% slower); the
           // gather runs only when the wave straddles groups
           const int sb0 = uniform(sb), db0 = uniform(db);
-          sbk[u] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb0));
-          sbv[u] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb0));
-          dbk[u] = reinterpret_cast<char*>(ld_const(p.dst_k_base + db0));
-          dbv[u] = reinterpret_cast<char*>(ld_const(p.dst_v_base + db0));
+          sbk[x] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb0));
+          sbv[x] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb0));
+          dbk[x] = reinterpret_cast<char*>(ld_const(p.dst_k_base + db0));
+          dbv[x] = reinterpret_cast<char*>(ld_const(p.dst_v_base + db0));
           if (!__all(sb == sb0 && db == db0)) {
-            sbk[u] = reinterpret_cast<const char*>(p.src_k_base[sb]);
-            sbv[u] = reinterpret_cast<const char*>(p.src_v_base[sb]);
-            dbk[u] = reinterpret_cast<char*>(p.dst_k_base[db]);
-            dbv[u] = reinterpret_cast<char*>(p.dst_v_base[db]);
+            sbk[x] = reinterpret_cast<const char*>(p.src_k_base[sb]);
+            sbv[x] = reinterpret_cast<const char*>(p.src_v_base[sb]);
+            dbk[x] = reinterpret_cast<char*>(p.dst_k_base[db]);
+            dbv[x] = reinterpret_cast<char*>(p.dst_v_base[db]);
           }
         }
-        live[u] = live[u] && span_u[u] >= 0;
         const bool aligned =
-            ((reinterpret_cast<uint64_t>(sbk[u]) | reinterpret_cast<uint64_t>(sbv[u]) |
-              reinterpret_cast<uint64_t>(dbk[u]) | reinterpret_cast<uint64_t>(dbv[u])) & 15u) == 0;
-        if (live[u] && !aligned) {
+            ((reinterpret_cast<uint64_t>(sbk[x]) | reinterpret_cast<uint64_t>(sbv[x]) |
+              reinterpret_cast<uint64_t>(dbk[x]) | reinterpret_cast<uint64_t>(dbv[x])) & 15u) == 0;
+        if (xl[x] && !aligned) {
           if (p.err != nullptr && (!UNIFORM || lane == 0)) atomicOr(p.err, MKV_FLAG_ALIGN);
-          live[u] = false;
+          xl[x] = false;
         }
       } else {
-        sbk[u] = p.s_k;
-        sbv[u] = p.s_v;
-        dbk[u] = p.d_k;
-        dbv[u] = p.d_v;
+        sbk[x] = p.s_k;
+        sbv[x] = p.s_v;
+        dbk[x] = p.d_k;
+        dbv[x] = p.d_v;
       }
-      s_at[u] += head_u[u] * p.src_hstride;
-      d_at[u] += head_u[u] * p.dst_hstride;
     }
 
     // ---- phase B: every data load of the workgroup's passes in flight at once
     __builtin_amdgcn_sched_barrier(0);
-    u32x4 kd[U], vd[U];
+    u32x4 kd[N], vd[N];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      kd[u] = u32x4{0, 0, 0, 0};
-      vd[u] = u32x4{0, 0, 0, 0};
-      if (live[u] && lane_live) {
-        kd[u] = load16(sbk[u] + s_at[u] + s_lane);
-        vd[u] = load16(sbv[u] + s_at[u] + s_lane);
+    for (int x = 0; x < N; ++x) {
+      const int u = x / LB;
+      kd[x] = u32x4{0, 0, 0, 0};
+      vd[x] = u32x4{0, 0, 0, 0};
+      if (xl[x] && lane_live) {
+        kd[x] = load16(sbk[x] + s_at[u] + s_lane);
+        vd[x] = load16(sbv[x] + s_at[u] + s_lane);
       }
     }
 #if MKV_TABLE_WITH_DATA
@@ -1005,21 +1043,22 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     // the partner exchange)
 #if MKV_V_FIRST
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (live[u] && lane_live) store16(dbv[u] + d_at[u] + d_lane, vd[u]);
+    for (int x = 0; x < N; ++x) {
+      if (xl[x] && lane_live) store16(dbv[x] + d_at[x / LB] + d_lane, vd[x]);
     }
 #endif
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool wave_rotates = UNIFORM ? (live[u] && delta_u[u] != 0 && p.rotary > 0)
+    for (int x = 0; x < N; ++x) {
+      const int u = x / LB, lb = x % LB;
+      const bool wave_rotates = UNIFORM ? (xl[x] && delta_u[u] != 0 && p.rotary > 0)
                                         : (p.rotary > 0);
       if (!wave_rotates) continue;
       u32x4 pd;
-      pd[0] = bpermute(partner_addr, kd[u][0]);
-      pd[1] = bpermute(partner_addr, kd[u][1]);
-      pd[2] = bpermute(partner_addr, kd[u][2]);
-      pd[3] = bpermute(partner_addr, kd[u][3]);
-      if (live[u] && lane_live && rot_lane && delta_u[u] != 0) {
+      pd[0] = bpermute(partner_addr, kd[x][0]);
+      pd[1] = bpermute(partner_addr, kd[x][1]);
+      pd[2] = bpermute(partner_addr, kd[x][2]);
+      pd[3] = bpermute(partner_addr, kd[x][3]);
+      if (xl[x] && lane_live && rot_lane && delta_u[u] != 0) {
         if constexpr (BATCHED) {
           if (span_u[u] != cur_span) {
             if constexpr (SMALL) {
@@ -1035,24 +1074,25 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
             cur_span = span_u[u];
           }
         }
-        kd[u] = Rotor<DT>::run(kd[u], pd, cs, sg, scale, rcp);
+        kd[x] = Rotor<DT>::run(kd[x], pd, cs, sg, scale[lb], rcp[lb]);
       }
     }
 
     // ---- phase D: stores (UNIFORM: the pass's destination row is wave-uniform, so the
     // stores go through buffer resources carrying the store cache policy)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (live[u] && lane_live) {
+    for (int x = 0; x < N; ++x) {
+      const int u = x / LB;
+      if (xl[x] && lane_live) {
         if constexpr (UNIFORM) {
-          store16_at(dbk[u] + d_at[u], d_lane, kd[u]);
+          store16_at(dbk[x] + d_at[u], d_lane, kd[x]);
 #if !MKV_V_FIRST
-          store16_at(dbv[u] + d_at[u], d_lane, vd[u]);
+          store16_at(dbv[x] + d_at[u], d_lane, vd[x]);
 #endif
         } else {
-          store16(dbk[u] + d_at[u] + d_lane, kd[u]);
+          store16(dbk[x] + d_at[u] + d_lane, kd[x]);
 #if !MKV_V_FIRST
-          store16(dbv[u] + d_at[u] + d_lane, vd[u]);
+          store16(dbv[x] + d_at[u] + d_lane, vd[x]);
 #endif
         }
       }
@@ -1190,11 +1230,13 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
   // tiles is rounded up to a multiple of MKV_XCDS below; extra workgroups exit at once
   if (tiles <= 0) return MKV_OK;
   if (MKV_XCDS > 1) tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
-  if (tiles > 0x7FFFFFFF || layers > 65535)
+  constexpr int LB = layer_batch<BATCHED, DIRECT>();
+  const int layer_groups = (layers + LB - 1) / LB;
+  if (tiles > 0x7FFFFFFF || layer_groups > 65535)
     return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
-                layers);
+                layer_groups);
   hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT>),
-                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layer_groups)),
                      dim3(kThreads), 0, stream, sp);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
@@ -1520,8 +1562,9 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
 template <int DT>
 int launch_small(const SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
   tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
+  constexpr int LB = layer_batch<true, true>();
   hipLaunchKernelGGL(shift_small_kernel<DT>,
-                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>((layers + LB - 1) / LB)),
                      dim3(kThreads), 0, stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
