@@ -638,6 +638,8 @@ def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
       16 to 2,048 tokens x 40 layers (flat store -> HND paged cache through shuffled
       slots, delta 186).  ``ShiftPlan`` takes the direct path by default up to
       ``DIRECT_MAX_TOKEN_LAYERS`` token-layers.
+    * ``span_count``: one shift of 16,384 tokens x 40 layers cut into 1, 64 or 4,096
+      spans (the plan pass builds the span prefix in every workgroup).
     """
     import torch
 
@@ -704,6 +706,39 @@ def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
         }
         del src, kv, plans, src_set, dst_set
         torch.cuda.empty_cache()
+
+    # the plan pass builds the span prefix in every workgroup: the same 16,384 tokens
+    # x 40 layers cut into 1, 64 and 4,096 (the limit of one descriptor) spans, each
+    # span with its own delta, flat store -> HND paged cache through shuffled slots
+    n = 16384
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    blocks = -(-n // bs) + 8
+    src = [torch.randn(n, heads, 2 * d, dtype=torch.bfloat16, device=dev, generator=gen)
+           for _ in range(layers)]
+    kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
+          for _ in range(layers)]
+    table = torch.randperm(blocks, device=dev, generator=gen)
+    pos = torch.arange(n, device=dev)
+    slot = table[pos // bs] * bs + pos % bs
+    src_set, dst_set = S.CacheSet([src], "flat"), S.CacheSet([kv], "hnd", bs)
+    out["span_count"] = {"what": "16,384 tokens x 40 layers (bf16) in 1, 64 or 4,096 spans, "
+                         "two-launch path; median launch time"}
+    plans = {}
+    for count in (1, 64, 4096):
+        per = n // count
+        rows = [(k * per, 0, 0, k * per, per, 186 + (k % 97), 0, 0) for k in range(count)]
+        plans[f"spans_{count}"] = S.ShiftPlan(
+            S.span_array(rows), src_set, dst_set, inv_freq=inv_freq_for(d, 1e6),
+            src_mode="flat", dst_mode="slots", dst_index=slot, direct=False)
+    warm_up(lambda: plans["spans_1"].launch(stream.cuda_stream))
+    ms = _ab(plans, max(steps, 30), warmup, stream)
+    gb = plans["spans_1"].algorithmic_bytes
+    for name, v in ms.items():
+        out["span_count"][name] = {"ms": round(v, 4),
+                                   "frac_of_peak": round(gb / (v / 1e3) / 1e9 / PEAK_GBS, 4)}
+    del src, kv, plans, src_set, dst_set
+    torch.cuda.empty_cache()
     return out
 
 
@@ -712,10 +747,11 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
     slot lists) into an HND paged cache.  Times the whole call from Python (store
     checks, span table, one pinned upload, plan + shift kernels) to the stream's
-    completion, next to the kernels alone on the same plan.  Two steps: the Qwen3-14B
-    multi-span workload's eight spans, and one 29,232-token load, the size of the
-    reference's in-engine measurement (docs/findings.md:664-666: 34.4 ms copy_ms,
-    6.2 ms of it the kernel)."""
+    completion, next to the kernels alone on the same plan.  Three steps: the Qwen3-14B
+    multi-span workload's eight spans in bf16 and in fp8 e4m3 (per-layer K scales, as
+    vLLM's ``_k_scale``), and one 29,232-token bf16 load, the size of the reference's
+    in-engine measurement (docs/findings.md:664-666: 34.4 ms copy_ms, 6.2 ms of it the
+    kernel)."""
     import numpy as np
     import torch
 
@@ -727,56 +763,68 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     layers, heads, d, bs = 40, 8, 128, 16
     lay = W.qwen3_14b_multispan_layout()
     history = lay.src_history
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0)
-    store = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
-    assert store.reserve("s", 0, history)
     names = [f"layer{i}" for i in range(layers)]
-    for name in names:
-        store.write_target("s", name, 0, history, (heads, 2 * d), torch.bfloat16,
-                           dev).normal_(generator=gen)
     blocks = -(-max(lay.dst_history, history) // bs) + 8
-    kv = {name: torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev)
-          for name in names}
     table = np.random.default_rng(1).permutation(blocks).astype(np.int32)
-    loader = ShiftLoader(store, bs, inv_freq_for(d, 1e6))
-    loader.register_kv_caches(kv)
-    cases = {
-        "qwen3_14b_8_spans": lambda: [
-            Load.from_blocks("s", table, int(dst), int(dst) + int(n), int(dl))
-            for dst, n, dl in zip(lay.dst_start, lay.length, lay.delta)],
-        "one_load_29232_tokens": lambda: [Load.from_blocks("s", table, 0, 29232, -186)],
-    }
     out = {"what": "ShiftLoader.start_load_kv from a BlockShiftStore session into an HND "
-           "paged cache (40 layers, bf16), block tables on the device; medians over steps",
+           "paged cache (40 layers), block tables on the device; medians over steps",
            "reference_in_engine_copy_ms_29232_tokens": 34.4,
            "reference_kernel_ms_29232_tokens": 6.2}
-    for case, loads in cases.items():
-        for _ in range(warmup):
-            loader.start_load_kv(loads())
-        torch.cuda.synchronize()
-        host, e2e = [], []
-        for _ in range(steps):
-            batch = loads()
+    multi = lambda: [Load.from_blocks("s", table, int(dst), int(dst) + int(n), int(dl))
+                     for dst, n, dl in zip(lay.dst_start, lay.length, lay.delta)]
+    for dtype, cases in (
+        (torch.bfloat16, {"qwen3_14b_8_spans": multi,
+                          "one_load_29232_tokens":
+                              lambda: [Load.from_blocks("s", table, 0, 29232, -186)]}),
+        (torch.float8_e4m3fn, {"qwen3_14b_8_spans_fp8": multi}),
+    ):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0)
+        fp8 = dtype == torch.float8_e4m3fn
+        k_scales = {}
+        if fp8:
+            ks, _ = W.fp8_layer_scales(5, layers)
+            k_scales = {name: float(k) for name, k in zip(names, ks)}
+        store = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
+        assert store.reserve("s", 0, history)
+        for name in names:
+            buf = store.write_target("s", name, 0, history, (heads, 2 * d), dtype, dev)
+            x = torch.randn(buf.shape, dtype=torch.float32, device=dev, generator=gen)
+            buf.copy_((x / k_scales[name]).clamp_(-448.0, 448.0) if fp8 else x)
+            del x
+        kv = {name: torch.zeros(blocks, heads, bs, 2 * d, dtype=dtype, device=dev)
+              for name in names}
+        loader = ShiftLoader(store, bs, inv_freq_for(d, 1e6), k_scales=k_scales)
+        loader.register_kv_caches(kv)
+        for case, loads in cases.items():
+            for _ in range(warmup):
+                loader.start_load_kv(loads())
             torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            loader.start_load_kv(batch)
-            t1 = time.perf_counter()
-            torch.cuda.synchronize()
-            e2e.append((time.perf_counter() - t0) * 1e3)
-            host.append((t1 - t0) * 1e3)
-        plan = loader.last_plan
-        _, per = time_plan(plan, steps, warmup, torch.cuda.current_stream(dev))
-        kms = float(np.mean(per))
-        out[case] = {
-            "tokens": plan.tokens,
-            "ms_end_to_end": round(float(np.median(e2e)), 4),
-            "host_ms": round(float(np.median(host)), 4),
-            "kernel_ms": round(kms, 4),
-            "kernel_GB_s": round(plan.algorithmic_bytes / (kms / 1e3) / 1e9, 1),
-        }
-    del store, kv, loader
-    torch.cuda.empty_cache()
+            host, e2e = [], []
+            for _ in range(steps):
+                batch = loads()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                loader.start_load_kv(batch)
+                t1 = time.perf_counter()
+                torch.cuda.synchronize()
+                e2e.append((time.perf_counter() - t0) * 1e3)
+                host.append((t1 - t0) * 1e3)
+            plan = loader.last_plan
+            _, per = time_plan(plan, steps, warmup, torch.cuda.current_stream(dev))
+            kms = float(np.mean(per))
+            out[case] = {
+                "dtype": "fp8_e4m3" if fp8 else "bf16",
+                "tokens": plan.tokens,
+                "ms_end_to_end": round(float(np.median(e2e)), 4),
+                "host_ms": round(float(np.median(host)), 4),
+                "kernel_ms": round(kms, 4),
+                "kernel_GB_s": round(plan.algorithmic_bytes / (kms / 1e3) / 1e9, 1),
+                "kernel_frac_of_peak": round(plan.algorithmic_bytes / (kms / 1e3) / 1e9
+                                             / PEAK_GBS, 4),
+            }
+        del store, kv, loader
+        torch.cuda.empty_cache()
     return out
 
 

@@ -169,9 +169,10 @@ typedef struct mkv_side {
  *                  that disagrees with the spans raises MKV_FLAG_SPAN; its tokens are
  *                  bounds-checked like any other.
  *   order        : MKV_ORDER_NONE, or MKV_ORDER_DST_PAGE: on the two-launch path, the
- *                  resolved tokens are sorted by the 2 MB page of their destination row
+ *                  resolved tokens are sorted by the page of their destination row (2 MB,
+ *                  or wider where the destination spans more than 256 such pages)
  *                  before the shift (a stable sort: the tokens of one page keep their
- *                  order; two more small launches), so that the workgroups running
+ *                  order; one more small launch), so that the workgroups running
  *                  together touch few destination pages.  The workspace then needs
  *                  MKV_ORDER_EXTRA_BYTES(total_tokens) more bytes.  Results are the same
  *                  bytes either way.  Ignored on the direct path.

@@ -702,7 +702,9 @@ class ShiftSaver:
         """``(row_shape, dtype, device, paged CacheSet)`` of a step's paged caches, worked
         out once per distinct tuple of cache tensors (vLLM passes the same ones every
         step)."""
-        key = tuple(caches)
+        # keyed by the tensors' ids (a tuple of tensors would hash each tensor through
+        # Python); the entry's CacheSet holds the tensors, so no id is reused meanwhile
+        key = tuple(map(id, caches))
         hit = self._geo.get(key)
         if hit is None:
             planes = [paged_planes(t, self.block_size) for t in caches]

@@ -190,6 +190,7 @@ struct PlanParams {
   TokRec* recs;   // [total_tokens]
   uint32_t* order_hist;  // ordered: [gridDim.x][kOrderBuckets] page counts per workgroup
   int64_t order_chunk;   // ordered: tokens per workgroup (contiguous)
+  int32_t order_shift;   // ordered: destination offset >> this = bucket
   int32_t* err;
   int64_t total_tokens;
   int32_t n_spans;
@@ -511,14 +512,16 @@ __device__ __forceinline__ int span_of(const int64_t* starts, int n_spans, int64
   return static_cast<int>(__popcll(__ballot(v <= g))) - 1;
 }
 
-// Destination-page order (MKV_ORDER_DST_PAGE): a record's bucket is the 2 MB page of its
-// destination row; pages past the last bucket share it.
-constexpr int kOrderBuckets = 1024;
+// Destination-page order (MKV_ORDER_DST_PAGE): a record's bucket is its destination row's
+// byte offset >> shift, where the host picks the smallest shift of at least 21 (2 MB
+// translation pages) that maps the destination cache's extent into kOrderBuckets
+// buckets; offsets past the last bucket share it.
+constexpr int kOrderBuckets = 256;
 constexpr int kOrderMaxGroups = 256;  // workgroups of an ordered plan pass (and scatter)
 
-__device__ __forceinline__ uint32_t order_bucket(const TokRec& r) {
+__device__ __forceinline__ uint32_t order_bucket(const TokRec& r, int shift) {
   if (r.span < 0) return 0;
-  const uint64_t page = static_cast<uint64_t>(r.dst_off) >> 21;
+  const uint64_t page = static_cast<uint64_t>(r.dst_off) >> shift;
   return page < kOrderBuckets ? static_cast<uint32_t>(page) : kOrderBuckets - 1;
 }
 
@@ -549,14 +552,42 @@ __device__ __forceinline__ void lane_tables(int delta, const float* inv_freq, in
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
   extern __shared__ int64_t s_pre[];  // [n_spans + 1]: exclusive prefix of tokens
   __shared__ int64_t s_part[kPlanThreads];
+  __shared__ int s_bad;
   const int tid = threadIdx.x;
   const int n = p.n_spans;
+  const bool checker = blockIdx.x == 0 && p.err != nullptr;  // workgroup 0 checks the spans
+  if (tid == 0) s_bad = 0;
 
+  // the spans' token counts into LDS: coalesced loads, 8 in flight per thread
+  constexpr int kStage = 8;
+  bool bad = false;
+  for (int i0 = 0; i0 < n; i0 += kStage * kPlanThreads) {
+    int32_t c[kStage];
+#pragma unroll
+    for (int k = 0; k < kStage; ++k) {
+      const int i = i0 + k * kPlanThreads + tid;
+      c[k] = i < n ? p.spans[i].n_tokens : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kStage; ++k) {
+      const int i = i0 + k * kPlanThreads + tid;
+      if (i < n) {
+        s_pre[i] = c[k] > 0 ? c[k] : 0;
+        if (checker) {
+          const mkv_span_t& sp = p.spans[i];
+          bad |= c[k] < 0 || sp.src_group < 0 || sp.src_group >= p.src.groups ||
+                 sp.dst_group < 0 || sp.dst_group >= p.dst.groups;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // exclusive prefix in place: per-thread contiguous chunks, then a scan of the chunks
   const int per = (n + kPlanThreads - 1) / kPlanThreads;
   const int b = tid * per;
   const int e = min(b + per, n);
   int64_t sum = 0;
-  for (int i = b; i < e; ++i) sum += max(p.spans[i].n_tokens, 0);
+  for (int i = b; i < e; ++i) sum += s_pre[i];
   s_part[tid] = sum;
   __syncthreads();
   for (int off = 1; off < kPlanThreads; off <<= 1) {
@@ -567,24 +598,19 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
   }
   int64_t run = s_part[tid] - sum;
   for (int i = b; i < e; ++i) {
+    const int64_t c = s_pre[i];
     s_pre[i] = run;
-    run += max(p.spans[i].n_tokens, 0);
+    run += c;
   }
   if (tid == kPlanThreads - 1) s_pre[n] = s_part[kPlanThreads - 1];
+  if (bad) s_bad = 1;
   __syncthreads();
   const int64_t actual = s_pre[n];
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kPlanThreads + tid;
   const int64_t gstride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
 
-  if (gtid == 0 && p.err != nullptr) {
-    bool bad = actual > p.total_tokens;
-    for (int i = 0; i < n; ++i) {
-      const mkv_span_t sp = p.spans[i];
-      bad |= sp.n_tokens < 0 || sp.src_group < 0 || sp.src_group >= p.src.groups ||
-             sp.dst_group < 0 || sp.dst_group >= p.dst.groups;
-    }
-    if (bad) atomicOr(p.err, MKV_FLAG_SPAN);
-  }
+  if (checker && tid == 0 && (s_bad != 0 || actual > p.total_tokens))
+    atomicOr(p.err, MKV_FLAG_SPAN);
 
   // cos / signed sin per span, element-indexed like the reference's tables
   const int half = p.rotary / 2;
@@ -658,7 +684,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
       }
     }
     p.recs[g] = r;
-    if (ordered) atomicAdd(&s_hist[order_bucket(r)], 1u);
+    if (ordered) atomicAdd(&s_hist[order_bucket(r, p.order_shift)], 1u);
   }
   if (ordered) {
     __syncthreads();
@@ -669,51 +695,51 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
 
 // -------------------------------------------------------------------- order kernels
 //
-// Optional (MKV_ORDER_DST_PAGE): the plan's records, sorted stably by the 2 MB page of
-// their destination row, so that the workgroups running together touch few destination
-// pages while the tokens of one destination block stay together and in order (each
-// record still carries its span, so the per-span tables are unchanged).  Three steps:
-// the ordered plan pass resolves one contiguous chunk of tokens per workgroup and counts
-// its pages; order_scan_kernel turns the counts, bucket-major, into each (page,
-// workgroup)'s first output position; order_scatter_kernel writes every chunk's records
-// there in token order (ranks within a wave from ballots, waves and batches in order).
+// Optional (MKV_ORDER_DST_PAGE): the plan's records, sorted stably by the page of their
+// destination row, so that the workgroups running together touch few destination pages
+// while the tokens of one destination block stay together and in order (each record
+// still carries its span, so the per-span tables are unchanged).  Two steps: the ordered
+// plan pass resolves one contiguous chunk of tokens per workgroup and counts its pages
+// ([groups][kOrderBuckets]); order_scatter_kernel, one workgroup per chunk, derives its
+// chunk's first output position in every page from all the counts and writes the
+// chunk's records there in token order (ranks within a wave from ballots, waves and
+// batches in order).
 
-constexpr int kScanThreads = kOrderBuckets;  // one thread per page bucket
-
-// hist: [groups][kOrderBuckets] page counts of each workgroup's chunk, rewritten as each
-// (workgroup, page)'s first output position, pages major: thread b walks bucket b down
-// the workgroups (coalesced across threads), then the buckets' totals are scanned.
-__global__ __launch_bounds__(kScanThreads) void order_scan_kernel(uint32_t* hist, int groups) {
-  __shared__ uint32_t part[kScanThreads];
-  const int b = threadIdx.x;
-  uint32_t total = 0;
-  for (int w = 0; w < groups; ++w) total += hist[static_cast<int64_t>(w) * kOrderBuckets + b];
-  part[b] = total;
-  __syncthreads();
-  for (int off = 1; off < kScanThreads; off <<= 1) {
-    const uint32_t v = b >= off ? part[b - off] : 0u;
-    __syncthreads();
-    part[b] += v;
-    __syncthreads();
-  }
-  uint32_t run = part[b] - total;
-  for (int w = 0; w < groups; ++w) {
-    uint32_t* h = hist + static_cast<int64_t>(w) * kOrderBuckets + b;
-    const uint32_t c = *h;
-    *h = run;
-    run += c;
-  }
-}
-
-constexpr int kScatterThreads = 256;
+constexpr int kScatterThreads = kOrderBuckets;  // thread b owns page bucket b
 
 __global__ __launch_bounds__(kScatterThreads) void order_scatter_kernel(
-    const TokRec* in, TokRec* out, const uint32_t* offsets, int64_t total, int64_t chunk) {
-  __shared__ uint32_t running[kOrderBuckets];  // records of each page placed so far
+    const TokRec* in, TokRec* out, const uint32_t* hist, int64_t total, int64_t chunk,
+    int groups, int shift) {
+  __shared__ uint32_t part[kOrderBuckets];     // records of each page, all chunks
+  __shared__ uint32_t running[kOrderBuckets];  // next output position of each page
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  for (int b = tid; b < kOrderBuckets; b += kScatterThreads) running[b] = 0;
+  // page tid: its records in every chunk, and in the chunks before this one (loads
+  // coalesced across threads, 32 chunks in flight per round)
+  constexpr int kRound = 32;
+  uint32_t all = 0, before = 0;
+  const int me = static_cast<int>(blockIdx.x);
+  for (int w = 0; w < groups; w += kRound) {
+    uint32_t c[kRound];
+#pragma unroll
+    for (int k = 0; k < kRound; ++k)
+      c[k] = w + k < groups ? hist[static_cast<int64_t>(w + k) * kOrderBuckets + tid] : 0u;
+#pragma unroll
+    for (int k = 0; k < kRound; ++k) {
+      all += c[k];
+      before += w + k < me ? c[k] : 0u;
+    }
+  }
+  part[tid] = all;
+  __syncthreads();
+  for (int off = 1; off < kOrderBuckets; off <<= 1) {  // inclusive scan over pages
+    const uint32_t v = tid >= off ? part[tid - off] : 0u;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  running[tid] = part[tid] - all + before;
   const int64_t lo = static_cast<int64_t>(blockIdx.x) * chunk;
   const int64_t hi = min(lo + chunk, total);
   const uint64_t below = (uint64_t{1} << lane) - 1;
@@ -722,11 +748,11 @@ __global__ __launch_bounds__(kScatterThreads) void order_scatter_kernel(
     const bool valid = g < hi;
     TokRec r{};
     if (valid) r = in[g];
-    const uint32_t key = valid ? order_bucket(r) : 0u;
+    const uint32_t key = valid ? order_bucket(r, shift) : 0u;
     uint32_t pos = 0;
-    __syncthreads();  // the previous batch's updates of `running` are done
-    for (int w = 0; w < kScatterThreads / 64; ++w) {
-      if (wave == w) {
+    __syncthreads();  // `running` is set (first batch) or the previous batch is done
+    for (int v = 0; v < kScatterThreads / 64; ++v) {
+      if (wave == v) {
         // the distinct pages of this wave, one ballot each, in lane order
         uint64_t todo = __ballot(valid);
         while (todo != 0) {
@@ -735,9 +761,7 @@ __global__ __launch_bounds__(kScatterThreads) void order_scatter_kernel(
               __builtin_amdgcn_readlane(static_cast<int>(key), leader));
           const uint64_t same = __ballot(valid && key == k);
           const uint32_t base = running[k];
-          if (valid && key == k)
-            pos = offsets[static_cast<int64_t>(blockIdx.x) * kOrderBuckets + k] + base +
-                  static_cast<uint32_t>(__popcll(same & below));
+          if (valid && key == k) pos = base + static_cast<uint32_t>(__popcll(same & below));
           if (lane == leader) running[k] = base + static_cast<uint32_t>(__popcll(same));
           todo &= ~same;
         }
@@ -1532,6 +1556,12 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
     pp.order_chunk = (d->total_tokens + groups - 1) / groups;
     sorted = recs + d->total_tokens;
     pp.order_hist = reinterpret_cast<uint32_t*>(sorted + d->total_tokens);
+    // the destination's extent per (group, layer), in bytes, sets the bucket width
+    const int64_t cap = pp.dst.num_slots > 0 ? pp.dst.num_slots : 0;
+    const int64_t extent = (cap / pp.dst.block_size + 1) * pp.dst.bstride;
+    int shift = 21;
+    while (shift < 62 && (extent >> shift) >= kOrderBuckets) ++shift;
+    pp.order_shift = shift;
   }
   const size_t lds = sizeof(int64_t) * (static_cast<size_t>(d->n_spans) + 1);
   hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kPlanThreads), lds,
@@ -1539,15 +1569,11 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "plan launch failed: %s", hipGetErrorString(e));
   if (ordered) {
-    hipLaunchKernelGGL(order_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, pp.order_hist,
-                       static_cast<int>(plan_grid));
+    hipLaunchKernelGGL(order_scatter_kernel, dim3(static_cast<unsigned>(plan_grid)),
+                       dim3(kScatterThreads), 0, st, recs, sorted, pp.order_hist,
+                       d->total_tokens, pp.order_chunk, static_cast<int>(plan_grid),
+                       pp.order_shift);
     e = hipGetLastError();
-    if (e == hipSuccess) {
-      hipLaunchKernelGGL(order_scatter_kernel, dim3(static_cast<unsigned>(plan_grid)),
-                         dim3(kScatterThreads), 0, st, recs, sorted, pp.order_hist,
-                         d->total_tokens, pp.order_chunk);
-      e = hipGetLastError();
-    }
     if (e != hipSuccess) return fail(MKV_ERR_HIP, "order launch failed: %s", hipGetErrorString(e));
     recs = sorted;
   }
