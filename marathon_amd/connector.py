@@ -200,7 +200,9 @@ class _SmallRunners:
 
 
 def _host(index) -> np.ndarray | None:
-    return None if index is None else index.numpy()
+    if index is None or isinstance(index, np.ndarray):
+        return index
+    return index.numpy()
 
 
 def _int32_table(t) -> np.ndarray:
@@ -242,7 +244,7 @@ def paged_index(items: list, block_size: int):
             tabs.append(win)
             rows.append((pos, off))
             off += win.size
-        return "table", torch.from_numpy(np.concatenate(tabs)), rows
+        return "table", tabs[0] if len(tabs) == 1 else np.concatenate(tabs), rows
     parts, rows, off = [], [], 0
     for it in items:
         if it.slots is None:
@@ -264,7 +266,7 @@ def _store_windows(store, items, start_of) -> tuple:
         tabs.append(win)
         rows.append((pos, off))
         off += win.size
-    return torch.from_numpy(np.concatenate(tabs)), rows
+    return tabs[0] if len(tabs) == 1 else np.concatenate(tabs), rows
 
 
 def detect_hnd(shape, block_size: int) -> bool:

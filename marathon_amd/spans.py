@@ -272,10 +272,13 @@ class ShiftPlan:
         stage = _Staging()
 
         def place(t: torch.Tensor | None, dtype: torch.dtype, np_dtype):
-            """A device tensor is used in place; a host one is staged.  Returns
+            """A device tensor is used in place; a host tensor or numpy array is staged.  Returns
             ``(device tensor or None, staging offset or None, count)``."""
             if t is None:
                 return None, None, 0
+            if isinstance(t, np.ndarray):  # host index windows built with numpy
+                a = t.reshape(-1)
+                return None, stage.add(a.astype(np_dtype, copy=False)), a.size
             t = t.detach().reshape(-1)
             if t.is_cuda:
                 t = t.to(device=self.device, dtype=dtype).contiguous()
@@ -487,6 +490,13 @@ class SmallShifts:
         self.modes = (src_mode, dst_mode)
         self.eligible_geometry = ShiftPlan.direct_eligible(src, dst, 1)
         self._idx = {"flat": (None, 0), "slots": (np.int64, 8), "table": (np.int32, 4)}
+        # the small entry point reads its host arrays during the call: one set of host
+        # buffers, addresses taken once, serves every step
+        self._h_spans = np.zeros(_lib.MKV_SMALL_MAX_SPANS, dtype=_lib.SPAN_DTYPE)
+        self._h_index = [np.zeros(_lib.MKV_SMALL_MAX_INDEX, dtype=self._idx[m][0] or np.int64)
+                         for m in (src_mode, dst_mode)]
+        self._h_addr = (self._h_spans.ctypes.data, self._h_index[0].ctypes.data,
+                        self._h_index[1].ctypes.data)
         self.capacity = 0
         self.buf = None
         self._keep = []
@@ -545,20 +555,22 @@ class SmallShifts:
         n_dst = 0 if dst_index is None else dst_index.size
         if (n <= _lib.MKV_SMALL_MAX_SPANS and n_src <= _lib.MKV_SMALL_MAX_INDEX
                 and n_dst <= _lib.MKV_SMALL_MAX_INDEX):
-            src_t, _ = self._idx[self.modes[0]]
-            dst_t, _ = self._idx[self.modes[1]]
-            spans = np.array(rows, dtype=_lib.SPAN_DTYPE)
-            si = None if not n_src else np.ascontiguousarray(src_index, dtype=src_t)
-            di = None if not n_dst else np.ascontiguousarray(dst_index, dtype=dst_t)
+            hs = self._h_spans
+            for i, r in enumerate(rows):
+                hs[i] = r
+            if n_src:
+                self._h_index[0][:n_src] = src_index
+            if n_dst:
+                self._h_index[1][:n_dst] = dst_index
             d = self.small_desc
-            d.spans = spans.ctypes.data
+            d.spans = self._h_addr[0]
             d.n_spans = n
             d.total_tokens = self.tokens = sum(max(int(r[4]), 0) for r in rows)
-            d.src.index = None if si is None else si.ctypes.data
+            d.src.index = self._h_addr[1] if n_src else None
             d.src.index_len = n_src
-            d.dst.index = None if di is None else di.ctypes.data
+            d.dst.index = self._h_addr[2] if n_dst else None
             d.dst.index_len = n_dst
-            self._last = (spans, si, di)  # a relaunch reads them again
+            self._last = (True,)  # a relaunch reads the host buffers again
             self.launch(error_flags=error_flags)
             return
         self._last = ()
