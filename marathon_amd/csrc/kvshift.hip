@@ -96,6 +96,15 @@
 #ifndef MKV_LAYERS_RECORDS
 #define MKV_LAYERS_RECORDS 1
 #endif
+// 1: the batched kernels fetch group 0's base addresses for their layers before the
+// token metadata (the usual single-session shift then needs no dependent fetch of
+// them).  Direct path, record path.
+#ifndef MKV_SPEC_BASE_DIRECT
+#define MKV_SPEC_BASE_DIRECT 1
+#endif
+#ifndef MKV_SPEC_BASE_RECORDS
+#define MKV_SPEC_BASE_RECORDS 0
+#endif
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs; with
 // the remap, XCD k walks the k-th contiguous eighth of the tiles (smaller per-XCD set
 // of pages in flight).  0 = plain order.
@@ -313,6 +322,17 @@ __device__ __forceinline__ T uniform(T v) {
   }
 }
 
+// The value lane `src` holds (src wave-uniform).
+__device__ __forceinline__ int32_t lane_value(int32_t v, int src) {
+  return __builtin_amdgcn_readlane(v, src);
+}
+__device__ __forceinline__ int64_t lane_value(int64_t v, int src) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(u & 0xFFFFFFFFu), src);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), src);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // RN(RN(k*c) + RN(kp*s)): the torch path's separate fp32 multiply, multiply, add
 // (shift_kernels.py:156).  `contract(off)` above keeps the compiler from fusing.
 __device__ __forceinline__ float rot1(float k, float kp, float c, float s) {
@@ -501,15 +521,6 @@ __device__ __forceinline__ bool resolve_direct(const DevSide& sd, const int64_t*
   }
   off_bytes = blk * sd.bstride + off * sd.ostride;
   return true;
-}
-
-// Wave-uniform: the span holding token g, the s with starts[s] <= g < starts[s + 1]
-// (n_spans <= 63): each lane reads one prefix entry, and a ballot counts the entries at
-// or below g.  -1 below the first span, n_spans past the last.  Every lane calls it.
-__device__ __forceinline__ int span_of(const int64_t* starts, int n_spans, int64_t g,
-                                       int lane) {
-  const int64_t v = lane <= n_spans ? starts[lane] : INT64_MAX;
-  return static_cast<int>(__popcll(__ballot(v <= g))) - 1;
 }
 
 // Destination-page order (MKV_ORDER_DST_PAGE): a record's bucket is its destination row's
@@ -878,6 +889,43 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
 #pragma unroll
   for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f / scale[lb];  // correctly rounded
 
+  // direct (span table in memory): lane k holds span k's fields and prefix entry k,
+  // loaded once; a pass finds its span with one ballot and reads the fields from that
+  // lane, with no dependent load
+  int64_t l_start = INT64_MAX, l_spos = 0, l_dpos = 0, l_sidx = 0, l_didx = 0;
+  int32_t l_n = 0, l_delta = 0, l_sg = 0, l_dg = 0;
+  if constexpr (DIRECT && !SMALL) {
+    if (lane <= p.n_spans) l_start = p.starts[lane];
+    if (lane < p.n_spans) {
+      const mkv_span_t sp = p.spans[lane];
+      l_spos = sp.src_pos;
+      l_dpos = sp.dst_pos;
+      l_sidx = sp.src_index;
+      l_didx = sp.dst_index;
+      l_n = sp.n_tokens;
+      l_delta = sp.delta;
+      l_sg = sp.src_group;
+      l_dg = sp.dst_group;
+    }
+  }
+  // group 0's base addresses for the workgroup's layers, fetched ahead (see
+  // MKV_SPEC_BASE_*); a pass of another group fetches its own
+  constexpr bool kSpec = BATCHED && UNIFORM &&
+                         (DIRECT ? MKV_SPEC_BASE_DIRECT != 0 : MKV_SPEC_BASE_RECORDS != 0);
+  const char* g0_sk[LB];
+  const char* g0_sv[LB];
+  char* g0_dk[LB];
+  char* g0_dv[LB];
+  if constexpr (kSpec) {
+#pragma unroll
+    for (int lb = 0; lb < LB; ++lb) {
+      g0_sk[lb] = reinterpret_cast<const char*>(ld_const(p.src_k_base + lay[lb]));
+      g0_sv[lb] = reinterpret_cast<const char*>(ld_const(p.src_v_base + lay[lb]));
+      g0_dk[lb] = reinterpret_cast<char*>(ld_const(p.dst_k_base + lay[lb]));
+      g0_dv[lb] = reinterpret_cast<char*>(ld_const(p.dst_v_base + lay[lb]));
+    }
+  }
+
   for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
     // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
     // metadata is fetched first, then all base addresses, so the workgroup pays two
@@ -900,21 +948,40 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
       if constexpr (DIRECT) {
         // the token's span and rows, resolved here from the span table (no plan pass)
         int s;
-        const int64_t* starts = SMALL ? q->starts : p.starts;
+        int64_t start, spos, dpos, sidx, didx;
+        int32_t n_tok, delta, sg, dg;
         if constexpr (SMALL) {
           s = -1;  // the prefix is the launch's own: a uniform scan of at most 9 entries
 #pragma unroll
           for (int k = 0; k <= MKV_SMALL_MAX_SPANS; ++k)
             if (k <= p.n_spans && q->starts[k] <= g) s = k;
+          const int sc = s >= 0 && s < p.n_spans ? s : 0;  // clamped: reads stay in range
+          const mkv_span_t* sp = q->spans + sc;
+          start = ld_const(q->starts + sc);
+          spos = ld_const(&sp->src_pos);
+          dpos = ld_const(&sp->dst_pos);
+          sidx = ld_const(&sp->src_index);
+          didx = ld_const(&sp->dst_index);
+          n_tok = ld_const(&sp->n_tokens);
+          delta = ld_const(&sp->delta);
+          sg = ld_const(&sp->src_group);
+          dg = ld_const(&sp->dst_group);
         } else {
-          s = span_of(p.starts, p.n_spans, g, lane);
+          s = static_cast<int>(__popcll(__ballot(l_start <= g))) - 1;
+          const int sc = s >= 0 && s < p.n_spans ? s : 0;
+          start = lane_value(l_start, sc);
+          spos = lane_value(l_spos, sc);
+          dpos = lane_value(l_dpos, sc);
+          sidx = lane_value(l_sidx, sc);
+          didx = lane_value(l_didx, sc);
+          n_tok = lane_value(l_n, sc);
+          delta = lane_value(l_delta, sc);
+          sg = lane_value(l_sg, sc);
+          dg = lane_value(l_dg, sc);
         }
-        const int sc = s >= 0 && s < p.n_spans ? s : 0;  // clamped: reads stay in range
-        const mkv_span_t* sp = (SMALL ? q->spans : p.spans) + sc;
-        const int64_t i = g - ld_const(starts + sc);
-        const int32_t sg = ld_const(&sp->src_group), dg = ld_const(&sp->dst_group);
-        const bool in_span = live[u] && s == sc && i >= 0;
-        bool ok = in_span && i < ld_const(&sp->n_tokens) && sg >= 0 && sg < p.src.groups &&
+        const int64_t i = g - start;
+        const bool in_span = live[u] && s >= 0 && s < p.n_spans && i >= 0;
+        bool ok = in_span && i < n_tok && sg >= 0 && sg < p.src.groups &&
                   dg >= 0 && dg < p.dst.groups;
         int64_t so = 0, dof = 0;
         if (ok) {
@@ -922,12 +989,10 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
                                                              : p.src.num_slots;
           const int64_t d_cap = p.dst.group_slots != nullptr ? ld_const(p.dst.group_slots + dg)
                                                              : p.dst.num_slots;
-          const bool s_ok = resolve_direct(p.src, SMALL ? q->src_index : nullptr, s_cap,
-                                           ld_const(&sp->src_pos), ld_const(&sp->src_index), i,
-                                           so);
-          const bool d_ok = resolve_direct(p.dst, SMALL ? q->dst_index : nullptr, d_cap,
-                                           ld_const(&sp->dst_pos), ld_const(&sp->dst_index), i,
-                                           dof);
+          const bool s_ok =
+              resolve_direct(p.src, SMALL ? q->src_index : nullptr, s_cap, spos, sidx, i, so);
+          const bool d_ok =
+              resolve_direct(p.dst, SMALL ? q->dst_index : nullptr, d_cap, dpos, didx, i, dof);
           if (!(s_ok && d_ok)) {
             if (p.err != nullptr && lane == 0)
               atomicOr(p.err, (s_ok ? 0 : MKV_FLAG_SRC_RANGE) | (d_ok ? 0 : MKV_FLAG_DST_RANGE));
@@ -937,7 +1002,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
           atomicOr(p.err, MKV_FLAG_SPAN);  // a bad group, or a prefix the spans do not fill
         }
         span_u[u] = ok ? s : -1;
-        delta_u[u] = ld_const(&sp->delta);
+        delta_u[u] = delta;
         s_at[u] = so;
         d_at[u] = dof;
         sb_u[u] = (ok ? sg : 0) * p.layers;
@@ -993,6 +1058,11 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
           sbv[x] = sbv[lb];
           dbk[x] = dbk[lb];
           dbv[x] = dbv[lb];
+        } else if (kSpec && sb_u[u] == 0 && db_u[u] == 0) {
+          sbk[x] = g0_sk[lb];
+          sbv[x] = g0_sv[lb];
+          dbk[x] = g0_dk[lb];
+          dbv[x] = g0_dv[lb];
         } else if (UNIFORM) {
           sbk[x] = reinterpret_cast<const char*>(ld_const(p.src_k_base + sb));
           sbv[x] = reinterpret_cast<const char*>(ld_const(p.src_v_base + sb));

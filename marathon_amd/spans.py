@@ -30,11 +30,18 @@ MODES = {"flat": _lib.MKV_ADDR_FLAT, "slots": _lib.MKV_ADDR_SLOTS, "table": _lib
 
 #: Shifts of at most this many (token, layer) rows take the library's direct path when
 #: eligible: one launch instead of the plan pass plus the shift.  Measured on MI355X
-#: (bf16, 8 heads, 40 layers): 1 and 16 tokens run in 6.8 and 7.1 us direct against
-#: 9.1 and 9.9 us; from 512 tokens the two-launch path is faster (0.036 against
-#: 0.043 ms), and at 8,192 tokens it streams 6.2 TB/s against 4.4, because a direct
-#: workgroup resolves its token through four dependent metadata reads before its data.
-DIRECT_MAX_TOKEN_LAYERS = 4096
+#: (bf16, 8 heads, 40 layers, one span, flat store -> HND cache through shuffled slots;
+#: bench.py's plan_variants): 16, 64 and 256 tokens run in 8.0, 9.6 and 21.6 us direct
+#: against 10.9, 12.6 and 22.2 us; from 512 tokens the two-launch path is faster (36.0
+#: against 36.9 us), and at 8,192 tokens it streams 6.2 TB/s against 5.4: a direct
+#: workgroup resolves its token (span, then slot) before it can load its data, where a
+#: record from the plan pass carries the token's rows.
+DIRECT_MAX_TOKEN_LAYERS = 10240
+#: SmallShifts puts a step's spans and index windows in the launch's own arguments up to
+#: this many (token, layer) rows: that saves the host its staging copy, but every
+#: workgroup then reads the arguments, which costs more than the copy from about 64
+#: tokens x 40 layers on (12.6 against 9.6 us of GPU time; 34 against 22 at 256).
+SMALL_ARGS_MAX_TOKEN_LAYERS = 2560
 
 
 #: Token orders of the two-launch path (``mkv_shift_desc_t.order``).
@@ -553,8 +560,10 @@ class SmallShifts:
         n = len(rows)
         n_src = 0 if src_index is None else src_index.size
         n_dst = 0 if dst_index is None else dst_index.size
+        tokens = sum(max(int(r[4]), 0) for r in rows)
         if (n <= _lib.MKV_SMALL_MAX_SPANS and n_src <= _lib.MKV_SMALL_MAX_INDEX
-                and n_dst <= _lib.MKV_SMALL_MAX_INDEX):
+                and n_dst <= _lib.MKV_SMALL_MAX_INDEX
+                and tokens * self.dst.layers <= SMALL_ARGS_MAX_TOKEN_LAYERS):
             hs = self._h_spans
             for i, r in enumerate(rows):
                 hs[i] = r
@@ -565,7 +574,7 @@ class SmallShifts:
             d = self.small_desc
             d.spans = self._h_addr[0]
             d.n_spans = n
-            d.total_tokens = self.tokens = sum(max(int(r[4]), 0) for r in rows)
+            d.total_tokens = self.tokens = tokens
             d.src.index = self._h_addr[1] if n_src else None
             d.src.index_len = n_src
             d.dst.index = self._h_addr[2] if n_dst else None

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from marathon_amd import _lib
-from marathon_amd.spans import CacheSet, SmallShifts
+from marathon_amd.spans import SMALL_ARGS_MAX_TOKEN_LAYERS, CacheSet, SmallShifts
 from oracle import kvshift_oracle as orc
 from tests.helpers import bits, dname, inv_freq, oracle_side, oracle_spans, randn
 
@@ -94,11 +94,12 @@ def test_small_steps_match_oracle(gpu, dtype, src_mode, dst_mode):
     # 1 token (a decode save), a few spans, then steps past the in-launch limits
     for n_spans, max_tokens in ((1, 1), (3, 12), (8, 6), (12, 5), (4, 30)):
         rows, si, di = _step(rng, src_mode, dst_mode, groups, n_spans, max_tokens)
+        tokens = sum(r[4] for r in rows)
         small = (n_spans <= _lib.MKV_SMALL_MAX_SPANS and di.size <= _lib.MKV_SMALL_MAX_INDEX
-                 and (si is None or si.size <= _lib.MKV_SMALL_MAX_INDEX))
+                 and (si is None or si.size <= _lib.MKV_SMALL_MAX_INDEX)
+                 and tokens * dst.layers <= SMALL_ARGS_MAX_TOKEN_LAYERS)
         print(f"case small step {dtype} {src_mode}->{dst_mode} spans={n_spans} "
               f"in-launch={small}", flush=True)
-        tokens = sum(r[4] for r in rows)
         assert runner.fits(n_spans, tokens)
         want = oracle_side(dst, dst_mode, torch.from_numpy(di))
         src_o = orc.Side(src_bits, src.layout, src.block_size, src_mode, si)
