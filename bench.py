@@ -52,6 +52,17 @@ PEAK_GBS = 8000.0  # MI355X HBM3E, decimal GB/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "shift_kernel_bf16_qwen3-14b-multispan_traffic.json")
 
 
+def build_defines() -> str:
+    """The tuning-knob definitions the library was built with ("" = the defaults)."""
+    from marathon_amd.build import DEFINES_FILE
+
+    try:
+        with open(DEFINES_FILE) as f:
+            return f.read().strip()
+    except OSError:
+        return "unknown"
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -1058,6 +1069,7 @@ def main() -> int:
             "spans": 8,
             "bytes_per_step": bytes_step,
         },
+        "build_defines": build_defines(),
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "tokens_per_s": round(tokens / (ms_step / 1e3), 1),
         "us_per_token": round(ms_step * 1e3 / tokens, 5),

@@ -52,11 +52,11 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (expected /opt/rocm/bin/hipcc)")
 
 
-def _compile(src: str, out: str, verbose: bool) -> str:
+def _compile(src: str, out: str, verbose: bool, extra: list | None = None) -> str:
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{os.path.join(HERE, 'csrc')}", src,
-           "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, *(extra or []), f"-I{INCLUDE}",
+           f"-I{os.path.join(HERE, 'csrc')}", src, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -71,8 +71,24 @@ def _compile(src: str, out: str, verbose: bool) -> str:
     return out
 
 
+#: Extra preprocessor definitions for the library's compile-time tuning knobs (the
+#: ``MKV_*`` macros at the top of ``csrc/kvshift.hip``), space-separated ``NAME=VALUE``
+#: pairs, e.g. ``MARATHON_KVSHIFT_DEFINES="MKV_STORE_CPOL=2 MKV_PASSES_2B=2"``: a build
+#: for an A/B of a default.  Empty: the defaults.
+DEFINES_ENV = "MARATHON_KVSHIFT_DEFINES"
+DEFINES_FILE = os.path.join(OUT_DIR, "build_defines.txt")
+
+
 def build_library(verbose: bool = False) -> str:
-    return _compile(SRC, OUT, verbose)
+    extra = [f"-D{d}" for d in os.environ.get(DEFINES_ENV, "").split() if d]
+    for d in extra:
+        if not d[2:].startswith("MKV_"):
+            raise ValueError(f"{DEFINES_ENV}: {d[2:]!r} is not an MKV_ tuning knob")
+    out = _compile(SRC, OUT, verbose, extra)
+    # beside the library, what it was built with (bench.py reports it)
+    with open(DEFINES_FILE, "w") as f:
+        f.write(" ".join(d[2:] for d in extra) + "\n")
+    return out
 
 
 def _compile_c_host(src: str, out: str, verbose: bool) -> str:

@@ -5,10 +5,8 @@
   it, and a random operation sequence is replayed on both stores side by side.
 * The allocator: lowest ids first, no block held twice, drop and eviction return
   blocks, growth never moves stored rows.
-* Under ``truncate=False`` validity is per position.  In the no-resave session that
-  the flat window corrupts (docs/single-request-load.md, "Design 2"), no load loses its
-  source.  A second failure that no store policy fixes is pinned as well: fresh saves
-  at their own index landing on drifted generation-0 bytes.
+* Under ``truncate=False`` validity is per position: a save below what is held keeps
+  the positions above it.
 """
 
 from __future__ import annotations
@@ -17,7 +15,6 @@ import numpy as np
 import torch
 
 from marathon_amd.block_store import BlockShiftStore
-from marathon_amd.remap import Remap, loads_for
 from marathon_amd.shift_store import ShiftStore, plan_load
 
 
@@ -243,82 +240,6 @@ def test_interval_policy_allows_holes_and_never_truncates():
     assert st.covers("a", 0, 100) and st.covers("a", 300, 50)
     assert st.reserve("a", 100, 200)  # filling the hole joins the intervals
     assert st.covers("a", 0, 350) and st.stats()["sessions"]["a"] == 350
-
-
-def _no_resave_session(truncate: bool, turns=20, seed=0):
-    """A paged session under no-resave (src/marathon/server.py:267-276), shaped like the
-    pager: every turn demotes the oldest live message to a stub, reuses everything after
-    it through the generation-0 book, and appends a user message plus a reply.  Only
-    what was computed this turn is saved, at its own positions.
-
-    Returns ``(lost, overwritten)``: loaded positions whose source the store no longer
-    holds, and loaded positions the store holds but whose bytes were written over by a
-    later save at the same index.
-    """
-    rng = np.random.default_rng(seed)
-    st = BlockShiftStore(budget_tokens=1 << 15, device="cpu", truncate=truncate)
-    next_id = [1000]
-
-    def fresh(n):
-        ids = list(range(next_id[0], next_id[0] + n))
-        next_id[0] += n
-        return ids
-
-    def save(lo, ids):
-        if ids and st.reserve("s", lo, len(ids)):
-            st.write("s", "l0", lo, torch.tensor(ids, dtype=torch.float32).reshape(-1, 1, 1))
-
-    msgs = [fresh(int(rng.integers(150, 300))) for _ in range(12)]
-    live = 0  # the oldest message not demoted yet
-    text = [t for m in msgs for t in m]
-    save(0, text)
-    book, lost, overwritten = Remap(), 0, 0
-    for _ in range(turns):
-        at = sum(len(m) for m in msgs[:live])
-        old_len = len(msgs[live])
-        msgs[live] = fresh(int(rng.integers(5, 20)))
-        live += 1
-        delta = len(msgs[live - 1]) - old_len
-        reused_hi = len(text) + delta  # everything after the stub, before the new text
-        msgs.append(fresh(int(rng.integers(20, 60))))  # the new user message
-        text = [t for m in msgs for t in m]
-        lo = at + len(msgs[live - 1])
-        for ld in loads_for(book, [{"dst_start": lo, "dst_end": reused_hi, "delta": delta}]):
-            src, n = ld["dst_start"] - ld["delta"], ld["dst_end"] - ld["dst_start"]
-            want = torch.tensor(text[ld["dst_start"]:ld["dst_end"]], dtype=torch.float32)
-            if not st.covers("s", src, n):
-                lost += n
-                continue
-            overwritten += int((st.read("s", "l0", src, n).reshape(-1) != want).sum())
-        book = book.after_turn([(lo, reused_hi, delta)], len(text))
-        save(at, msgs[live - 1])  # the stub, at its own positions
-        save(reused_hi, text[reused_hi:])  # the new user message
-        reply = fresh(int(rng.integers(10, 40)))
-        msgs[-1] = msgs[-1] + reply
-        save(len(text), reply)
-        text = text + reply
-    return lost, overwritten
-
-
-def test_per_position_validity_keeps_what_truncation_loses():
-    """The measured blocker (docs/single-request-load.md, "Design 2"): under the flat
-    window, the stub saved low in the history truncates the generation-0 bytes above it,
-    and later loads find their source gone.  Per-position validity loses nothing."""
-    lost_flat, _ = _no_resave_session(truncate=True)
-    lost_blocks, _ = _no_resave_session(truncate=False)
-    assert lost_flat > 0
-    assert lost_blocks == 0
-
-
-def test_fresh_saves_at_their_own_index_can_overwrite_generation_zero_bytes():
-    """What per-position validity does not fix.  After the text shrinks, the new text
-    appended at its own indices lands where a drifted span's generation-0 bytes still
-    live.  A later load then reads the wrong tokens with every position "valid".  So
-    generation-0 reuse also needs fresh KV stored away from every drifted span's
-    source.  This is a property of the address book, not of any store; it is pinned
-    here so the limit stays visible."""
-    _, overwritten = _no_resave_session(truncate=False)
-    assert overwritten > 0
 
 
 def test_lookup_layers_matches_per_layer_lookups():
