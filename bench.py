@@ -944,8 +944,8 @@ def main() -> int:
                     help="skip the A/B of record order and of the direct path")
     ap.add_argument("--only", default="",
                     help="comma-separated informational sections to run (e.g. "
-                    "'plan_variants'); every other one, the CPU baseline included, is "
-                    "skipped")
+                    "'plan_variants'; 'headline' for none); every other one, the CPU "
+                    "baseline included, is skipped")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (for PMC counter scaling)")
     args = ap.parse_args()
@@ -954,7 +954,7 @@ def main() -> int:
         sections = {"reference_shape", "reference_loop", "other_workloads", "tp_shares",
                     "size_sweep", "ceilings", "dst_layouts", "connector_step",
                     "plan_variants", "cpu_baseline"}
-        if keep - sections:
+        if keep - sections - {"headline"}:  # "headline": the headline line alone
             ap.error(f"--only: unknown sections {sorted(keep - sections)}")
         for name in sections - keep:
             setattr(args, "no_" + name, True)
