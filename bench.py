@@ -794,7 +794,7 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
         fp8 = dtype == torch.float8_e4m3fn
         k_scales = {}
         if fp8:
-            ks, _ = W.fp8_layer_scales(5, layers)
+            ks, _ = W.fp8_layer_scales(4, layers)  # the fp8 multi-span shift's scales
             k_scales = {name: float(k) for name, k in zip(names, ks)}
         store = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
         assert store.reserve("s", 0, history)
