@@ -51,7 +51,7 @@ def _layer_rows(wl, layer, spans, src_slots, dst_slots):
     return torch.cat(src_parts), torch.cat(dst_parts)
 
 
-def _check_full(wl, dtype_name, snapshot=True, threads=16):
+def _check_full(wl, dtype_name, snapshot=True, threads=16, **plan_kw):
     """Every row of every span and layer: V bit-exact (compared on the device), K
     bit-exact against the oracle's C restatement (computed layer by layer on the host),
     untouched slots unchanged.  snapshot=False: the destination started all-zero (saves
@@ -59,7 +59,7 @@ def _check_full(wl, dtype_name, snapshot=True, threads=16):
     dev = wl.dst.first.device
     snapshot = [c.clone() for c in wl.dst.caches[0]] if snapshot else None
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
-    wl.plan().launch(error_flags=flags)
+    wl.plan(**plan_kw).launch(error_flags=flags)
     torch.cuda.synchronize(dev)
     assert int(flags.item()) == 0
     _compare_full(wl, dtype_name, snapshot, threads)
@@ -132,6 +132,16 @@ def test_qwen3_14b_multispan_fp8_full_size(gpu):
     print("case Qwen3-14B multi-span fp8 full size", flush=True)
     wl = W.qwen3_14b_multispan_fp8(gpu)
     _check_full(wl, "fp8")
+    del wl
+    torch.cuda.empty_cache()
+
+
+def test_qwen3_14b_multispan_fp8_full_size_in_page_order(gpu):
+    """The same shift with its tokens sorted by destination page (order="dst_page"):
+    every row lands where span order puts it."""
+    print("case Qwen3-14B multi-span fp8 full size, destination-page order", flush=True)
+    wl = W.qwen3_14b_multispan_fp8(gpu)
+    _check_full(wl, "fp8", order="dst_page")
     del wl
     torch.cuda.empty_cache()
 

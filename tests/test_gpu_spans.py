@@ -594,3 +594,33 @@ def test_direct_path_flags_a_prefix_that_disagrees_with_the_spans(gpu):
         ok = (got == tokens(before[layer])).all(axis=(-1, -2)) | (
             got == tokens(dst_o.caches[0][layer])).all(axis=(-1, -2))
         assert bool(ok.all()), f"layer {layer}: a row is neither untouched nor the oracle's"
+
+
+def test_page_order_over_a_destination_wider_than_256_pages(gpu):
+    """A 590 MB destination cache (9,000 HND blocks of 64 KB): the page order's buckets
+    widen to 4 MB so the extent fits 256 of them.  Sorted and span-ordered plans write
+    the oracle's bytes."""
+    from marathon_amd.spans import CacheSet, ShiftPlan
+
+    print("case page order over a 590 MB destination", flush=True)
+    rng = np.random.default_rng(23)
+    g = torch.Generator().manual_seed(23)
+    heads, d, bs, blocks, n = 8, 128, 16, 9000, 3000
+    src = [torch.randn(4096, heads, 2 * d, generator=g).to(torch.bfloat16).to(gpu)]
+    kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=gpu)]
+    assert kv[0].numel() * 2 > 512 << 20
+    dst_slots = torch.from_numpy(rng.permutation(blocks * bs)[:n].astype(np.int64))
+    rows = [(0, 0, 0, 0, 1000, 77, 0, 0), (1500, 0, 0, 1000, 2000, -901, 0, 0)]
+    src_o = oracle_side(CacheSet([src], "flat"), "flat", None)
+    dst_o = oracle_side(CacheSet([kv], "hnd", bs), "slots", dst_slots)
+    orc.shift_spans(oracle_spans(span_array(rows)), src_o, dst_o, inv_freq().numpy(), "bf16")
+    for order in ("none", "dst_page"):
+        kv[0].zero_()
+        plan = ShiftPlan(span_array(rows), CacheSet([src], "flat"), CacheSet([kv], "hnd", bs),
+                         inv_freq=inv_freq(), src_mode="flat", dst_mode="slots",
+                         dst_index=dst_slots, direct=False, order=order)
+        flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+        plan.launch(error_flags=flags)
+        torch.cuda.synchronize(gpu)
+        assert int(flags.item()) == 0
+        assert np.array_equal(bits(kv[0]), dst_o.caches[0][0]), order
