@@ -88,10 +88,15 @@
 #ifndef MKV_STORE_CPOL
 #define MKV_STORE_CPOL 18
 #endif
-// Layers one workgroup of the batched kernels moves (grid.y = ceil(layers / this)): the
-// token metadata of a pass is resolved once for all of them.  Direct path, record path.
-#ifndef MKV_LAYERS_DIRECT
-#define MKV_LAYERS_DIRECT 1
+// Layers one workgroup moves (grid.y = ceil(layers / this)), each pass's token metadata
+// resolved once for all of them.  The direct path moves MKV_DIRECT_WIDE_LAYERS layers per
+// workgroup when a shift of 2- or 4-byte elements has more than MKV_DIRECT_WIDE_MIN_ROWS
+// (token, layer) rows, and one layer otherwise; the record path MKV_LAYERS_RECORDS.
+#ifndef MKV_DIRECT_WIDE_LAYERS
+#define MKV_DIRECT_WIDE_LAYERS 4
+#endif
+#ifndef MKV_DIRECT_WIDE_MIN_ROWS
+#define MKV_DIRECT_WIDE_MIN_ROWS 2560
 #endif
 #ifndef MKV_LAYERS_RECORDS
 #define MKV_LAYERS_RECORDS 1
@@ -117,9 +122,10 @@ namespace {
 constexpr int kThreads = MKV_WG_THREADS;  // shift kernel; a multiple of the 64-lane wave
 constexpr int kWaves = kThreads / 64;
 
-template <bool BATCHED, bool DIRECT>
+// layers per workgroup of the record path (the direct path picks its own per launch)
+template <bool BATCHED>
 constexpr int layer_batch() {
-  return !BATCHED ? 1 : DIRECT ? MKV_LAYERS_DIRECT : MKV_LAYERS_RECORDS;
+  return BATCHED ? MKV_LAYERS_RECORDS : 1;
 }
 constexpr int kPlanThreads = 256;  // plan kernel
 // Buffer resources for the stores: raw (stride 0), the whole 32-bit range checked by
@@ -790,14 +796,14 @@ __global__ __launch_bounds__(kScatterThreads) void order_scatter_kernel(
 // (token, head) rows.  UNIFORM: heads % rpw == 0, so every row of a pass belongs to
 // one token.
 
-template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, bool SMALL>
+template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, bool SMALL, int LB>
 __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack* q) {
   static_assert(!DIRECT || (BATCHED && UNIFORM), "direct shifts resolve one token per pass");
   static_assert(!SMALL || DIRECT, "small shifts take the direct path");
   using E = Elem<DT>;
   constexpr int C = E::kPerChunk;
   constexpr int U = E::kPasses;
-  constexpr int LB = layer_batch<BATCHED, DIRECT>();
+  static_assert(LB >= 1 && (BATCHED || LB == 1), "one layer per single-span launch");
   constexpr int N = U * LB;  // (pass, layer) units of one sweep: x = u * LB + lb
 
   const int tid = threadIdx.x;
@@ -1194,15 +1200,15 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   }
 }
 
-template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT>
+template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, int LB>
 __global__ __launch_bounds__(kThreads) void shift_kernel(ShiftParams p) {
-  shift_body<DT, BATCHED, UNIFORM, DIRECT, false>(p, nullptr);
+  shift_body<DT, BATCHED, UNIFORM, DIRECT, false, LB>(p, nullptr);
 }
 
 // A small shift: the span table, prefix and index windows arrive in the arguments.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void shift_small_kernel(SmallParams a) {
-  shift_body<DT, true, true, true, true>(a.p, &a.q);
+  shift_body<DT, true, true, true, true, 1>(a.p, &a.q);
 }
 
 // --------------------------------------------------------------------- host side
@@ -1319,17 +1325,16 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_
   return MKV_OK;
 }
 
-template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT>
+template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, int LB>
 int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t stream) {
   // tiles is rounded up to a multiple of MKV_XCDS below; extra workgroups exit at once
   if (tiles <= 0) return MKV_OK;
   if (MKV_XCDS > 1) tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
-  constexpr int LB = layer_batch<BATCHED, DIRECT>();
   const int layer_groups = (layers + LB - 1) / LB;
   if (tiles > 0x7FFFFFFF || layer_groups > 65535)
     return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
                 layer_groups);
-  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT>),
+  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT, LB>),
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layer_groups)),
                      dim3(kThreads), 0, stream, sp);
   const hipError_t e = hipGetLastError();
@@ -1337,15 +1342,26 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
   return MKV_OK;
 }
 
+// direct_layers: the direct path's layers per workgroup (1, or MKV_DIRECT_WIDE_LAYERS for
+// a larger shift of 2-byte or 4-byte elements); 0 = the record path.
 template <bool BATCHED>
-int launch_any(int dtype, bool uniform, bool direct, const ShiftParams& sp, int64_t tiles,
-               int layers, hipStream_t stream) {
-#define MKV_CASE(DT)                                                                     \
-  case DT:                                                                               \
-    if (BATCHED && uniform && direct)                                                    \
-      return launch_shift<DT, BATCHED, BATCHED, BATCHED>(sp, tiles, layers, stream);    \
-    return uniform ? launch_shift<DT, BATCHED, true, false>(sp, tiles, layers, stream)   \
-                   : launch_shift<DT, BATCHED, false, false>(sp, tiles, layers, stream);
+int launch_any(int dtype, bool uniform, int direct_layers, const ShiftParams& sp,
+               int64_t tiles, int layers, hipStream_t stream) {
+  constexpr int RL = layer_batch<BATCHED>();
+#define MKV_CASE(DT)                                                                        \
+  case DT:                                                                                  \
+    if constexpr (BATCHED) {                                                                \
+      if (uniform && direct_layers > 0) {                                                   \
+        if constexpr (DT != MKV_FP8_E4M3 && MKV_DIRECT_WIDE_LAYERS > 1) {                   \
+          if (direct_layers > 1)                                                            \
+            return launch_shift<DT, true, true, true, MKV_DIRECT_WIDE_LAYERS>(sp, tiles,    \
+                                                                              layers, stream); \
+        }                                                                                   \
+        return launch_shift<DT, true, true, true, 1>(sp, tiles, layers, stream);            \
+      }                                                                                     \
+    }                                                                                       \
+    return uniform ? launch_shift<DT, BATCHED, true, false, RL>(sp, tiles, layers, stream)  \
+                   : launch_shift<DT, BATCHED, false, false, RL>(sp, tiles, layers, stream);
   switch (dtype) {
     MKV_CASE(MKV_BF16)
     MKV_CASE(MKV_F16)
@@ -1499,7 +1515,7 @@ extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
   sp.heads_magic = g.heads_magic;
   sp.rotate = rot ? 1 : 0;
   const int64_t tiles = (n_tokens + g.tile_tokens - 1) / g.tile_tokens;
-  return launch_any<false>(dtype, g.uniform, false, sp, tiles, 1,
+  return launch_any<false>(dtype, g.uniform, 0, sp, tiles, 1,
                            static_cast<hipStream_t>(stream));
 }
 
@@ -1564,7 +1580,11 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
     sp.starts = d->span_starts;
     sp.n_spans = d->n_spans;
     sp.tables = d->span_tables;
-    return launch_any<true>(d->dtype, true, true, sp, tiles, d->layers, st);
+    const int direct_layers =
+        d->dtype != MKV_FP8_E4M3 && d->total_tokens * d->layers > MKV_DIRECT_WIDE_MIN_ROWS
+            ? MKV_DIRECT_WIDE_LAYERS
+            : 1;
+    return launch_any<true>(d->dtype, true, direct_layers, sp, tiles, d->layers, st);
   }
 
   if (d->order != MKV_ORDER_NONE && d->order != MKV_ORDER_DST_PAGE)
@@ -1652,15 +1672,14 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   sp.tables = tables;
   sp.src_hstride = src_hs;
   sp.dst_hstride = dst_hs;
-  return launch_any<true>(d->dtype, g.uniform, false, sp, tiles, d->layers, st);
+  return launch_any<true>(d->dtype, g.uniform, 0, sp, tiles, d->layers, st);
 }
 
 template <int DT>
 int launch_small(const SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
   tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
-  constexpr int LB = layer_batch<true, true>();
   hipLaunchKernelGGL(shift_small_kernel<DT>,
-                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>((layers + LB - 1) / LB)),
+                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
                      dim3(kThreads), 0, stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));

@@ -31,12 +31,12 @@ MODES = {"flat": _lib.MKV_ADDR_FLAT, "slots": _lib.MKV_ADDR_SLOTS, "table": _lib
 #: Shifts of at most this many (token, layer) rows take the library's direct path when
 #: eligible: one launch instead of the plan pass plus the shift.  Measured on MI355X
 #: (bf16, 8 heads, 40 layers, one span, flat store -> HND cache through shuffled slots;
-#: bench.py's plan_variants): 16, 64 and 256 tokens run in 8.0, 9.6 and 21.6 us direct
-#: against 10.9, 12.6 and 22.2 us; from 512 tokens the two-launch path is faster (36.0
-#: against 36.9 us), and at 8,192 tokens it streams 6.2 TB/s against 5.4: a direct
-#: workgroup resolves its token (span, then slot) before it can load its data, where a
-#: record from the plan pass carries the token's rows.
-DIRECT_MAX_TOKEN_LAYERS = 10240
+#: bench.py's plan_variants): 16, 64, 256 and 512 tokens run in 6.6, 8.8, 21.8 and
+#: 34.3 us direct against 10.2, 11.9, 22.5 and 36.8 us; from 1,024 tokens the two-launch
+#: path is faster (61.6 against 63.5 us): a direct workgroup resolves its token (span,
+#: then slot) before it can load its data, where a record from the plan pass carries the
+#: token's rows.  Above 2,560 rows the direct kernel moves four layers per workgroup.
+DIRECT_MAX_TOKEN_LAYERS = 20480
 #: SmallShifts puts a step's spans and index windows in the launch's own arguments up to
 #: this many (token, layer) rows: that saves the host its staging copy, but every
 #: workgroup then reads the arguments, which costs more than the copy from about 64

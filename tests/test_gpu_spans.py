@@ -16,7 +16,7 @@ from marathon_amd import workloads as W
 from marathon_amd.connector import Load, ShiftLoader
 from marathon_amd.spans import span_array
 from oracle import kvshift_oracle as orc
-from tests.helpers import bits, dname, inv_freq, oracle_side, oracle_spans
+from tests.helpers import bits, dname, inv_freq, oracle_side, oracle_spans, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -624,3 +624,44 @@ def test_page_order_over_a_destination_wider_than_256_pages(gpu):
         torch.cuda.synchronize(gpu)
         assert int(flags.item()) == 0
         assert np.array_equal(bits(kv[0]), dst_o.caches[0][0]), order
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float8_e4m3fn])
+@pytest.mark.parametrize("layers", [6, 9])
+def test_direct_path_above_the_wide_threshold(gpu, dtype, layers):
+    """A direct shift of more than 2,560 (token, layer) rows: 2- and 4-byte elements move
+    four layers per workgroup, so 6 and 9 layers leave a partial last group (fp8 stays at
+    one layer per workgroup).  Every destination byte against the oracle."""
+    from marathon_amd.spans import CacheSet, ShiftPlan
+
+    eb = torch.empty(0, dtype=dtype).element_size()
+    heads = 64 // (128 * eb // 16)  # the smallest head count the direct path takes
+    print(f"case wide direct shift {dtype} heads={heads} layers={layers}", flush=True)
+    rng = np.random.default_rng(layers)
+    g = torch.Generator().manual_seed(layers)
+    d, bs, hist, blocks = 128, 16, 1200, 120
+    k_scale = None
+    if dtype == torch.float8_e4m3fn:
+        k_scale = torch.from_numpy(rng.uniform(0.01, 0.1, layers).astype(np.float32))
+    src = [randn((hist, heads, 2 * d), dtype, g,
+                 1.0 if k_scale is None else float(k_scale[i])).to(gpu) for i in range(layers)]
+    kv = [torch.zeros(blocks, heads, bs, 2 * d, dtype=dtype, device=gpu) for _ in range(layers)]
+    n = 700
+    dst_slots = torch.from_numpy(rng.permutation(blocks * bs)[:n].astype(np.int64))
+    rows = [(0, 0, 0, 0, 300, 45, 0, 0), (500, 0, 0, 300, 250, -2000, 0, 0),
+            (900, 0, 0, 550, 150, 0, 0, 0)]
+    assert n * layers > 2560
+    src_set, dst_set = CacheSet([src], "flat"), CacheSet([kv], "hnd", bs)
+    plan = ShiftPlan(span_array(rows), src_set, dst_set, inv_freq=inv_freq(), src_mode="flat",
+                     dst_mode="slots", dst_index=dst_slots, k_scale=k_scale, direct=True)
+    assert plan.direct
+    src_o = oracle_side(src_set, "flat", None)
+    dst_o = oracle_side(dst_set, "slots", dst_slots)
+    orc.shift_spans(oracle_spans(span_array(rows)), src_o, dst_o, inv_freq().numpy(),
+                    dname(dtype), None if k_scale is None else k_scale.numpy())
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer in range(layers):
+        assert np.array_equal(bits(kv[layer]), dst_o.caches[0][layer]), f"layer {layer}"
