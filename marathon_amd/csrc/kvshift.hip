@@ -25,10 +25,15 @@
 //     loads.
 //   * rotate_half needs chunk j +- rotary/2: it comes from the partner lane through
 //     ds_bpermute (no second global read of K).
-//   * Batched shifts first run a small plan kernel that resolves every token's source
-//     and destination row (slot arrays / block tables, bounds-checked) into a record,
-//     and evaluates each span's cos/sin once (double precision, rounded to fp32).
-//     Both live in a caller-provided workspace; the library allocates nothing.
+//   * Batched shifts take one of three paths.  Two launches: a small plan kernel
+//     resolves every token's source and destination row (slot arrays / block tables,
+//     bounds-checked) into a record and evaluates each span's cos/sin once (double
+//     precision, rounded to fp32), both in a caller-provided workspace; the shift kernel
+//     then reads one record per token (optionally sorted by destination page first).
+//     Direct (short shifts, caller-supplied prefix and tables): the shift kernel alone,
+//     each workgroup resolving its token from the span table, whose entries the wave's
+//     lanes hold in registers.  Small (a decode step): the spans and index windows
+//     travel in the launch's arguments.  The library allocates nothing.
 //   * Loads and stores are non-temporal: every byte is touched exactly once.  Where a
 //     pass's destination row is wave-uniform, the stores also carry device scope
 //     (sc1 nt, through a buffer resource), measured 2-3% faster for these write-once
@@ -791,10 +796,13 @@ __global__ __launch_bounds__(kScatterThreads) void order_scatter_kernel(
 
 // -------------------------------------------------------------------- shift kernel
 //
-// Grid (token tiles, layers).  Wave w of the workgroup runs passes q = w + kWaves * u
-// (u < U); pass q covers rows [q * rpw, (q + 1) * rpw) of the tile's token-major
-// (token, head) rows.  UNIFORM: heads % rpw == 0, so every row of a pass belongs to
-// one token.
+// Grid (token tiles, layer groups of LB layers).  Wave w of the workgroup runs passes
+// q = w + kWaves * u (u < U); pass q covers rows [q * rpw, (q + 1) * rpw) of the tile's
+// token-major (token, head) rows, in each of the workgroup's LB layers.  UNIFORM:
+// heads % rpw == 0, so every row of a pass belongs to one token.  BATCHED: a span
+// table (records from the plan pass, or DIRECT: resolved here); otherwise one span of
+// one layer (mkv_scatter_shifted).  SMALL: the span table and index windows are the
+// launch's arguments.
 
 template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, bool SMALL, int LB>
 __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack* q) {
