@@ -1000,6 +1000,7 @@ def main() -> int:
     value = bytes_step * args.steps / wall / 1e9
     ev_ms = float(np.mean(per))
     achieved = bytes_step / (ev_ms / 1e3) / 1e9
+    metadata = plan.metadata_bytes
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -1081,6 +1082,8 @@ def main() -> int:
             "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic,
             "kernel_ms": round(ev_ms, 4),
+            # not in `achieved`: span and index arrays, rotation tables, token records
+            "metadata_bytes": metadata,
         },
         "cpu_baseline": cpu,
         "qwen3_0_6b_shift_hip": small,

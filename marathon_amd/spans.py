@@ -5,7 +5,10 @@ The reference issues one Triton launch per layer per load
 layer per segment (src/marathon/kvshift.py:242-268).  Here a :class:`ShiftPlan` holds a
 device-resident span table (``mkv_span_t``), per-(group, layer) base-address tables for
 source and destination, and the slot/block-table arrays, and :meth:`ShiftPlan.launch`
-enqueues the whole shift as one ``mkv_shift_spans`` call.
+enqueues the whole shift as one ``mkv_shift_spans`` call: a plan launch plus the shift
+(optionally with the tokens sorted by destination page), or, for short shifts, the shift
+alone (the direct path).  :class:`SmallShifts` runs the steady state of a serving loop --
+a decode step's saves, short loads -- with no plan to build.
 
 Caches are described by :class:`CacheSet`: ``caches[group][layer]`` tensors of one
 layout -- ``flat`` ``[rows, heads, 2D]`` (a position-indexed store, the reference's
@@ -229,18 +232,21 @@ class ShiftPlan:
     (mode ``table``) or ``None`` (mode ``flat``), on the host or the device.
     ``inv_freq``: fp32 [rotary / 2].  ``k_scale``: fp32 [layers] for fp8 caches.
 
-    Everything host-side (span table, per-(group, layer) base addresses, host index
-    arrays, tables) goes to the device in one pinned, stream-ordered copy, so building
-    a plan never blocks on the GPU.
+    Everything host-side (span table, host index arrays, inv_freq, scales, the direct
+    path's prefix and tables) goes to the device in one pinned, stream-ordered copy, so
+    building a plan never blocks on the GPU; the caches' base-address tables are
+    uploaded once per :class:`CacheSet`.
 
-    ``direct``: None (default) takes the library's single-launch path whenever
-    :meth:`direct_eligible` allows it, with the token prefix and the per-span rotation
-    tables computed here (:func:`span_tables`); False always runs the two-launch path
-    (plan pass and workspace), True asks for the direct path where eligible.
+    ``direct``: None (default) takes the library's single-launch path up to
+    :data:`DIRECT_MAX_TOKEN_LAYERS` rows whenever :meth:`direct_eligible` allows it,
+    with the token prefix and the per-span rotation tables computed here
+    (:func:`span_tables`); False always runs the two-launch path (plan pass and
+    workspace), True asks for the direct path where eligible.
 
     ``order``: the order the two-launch path moves tokens in -- ``"none"`` (span order)
-    or ``"dst_page"`` (sorted by the 2 MB page of each token's destination row, one
-    more small launch); None takes :data:`DEFAULT_ORDER` for the element type.
+    or ``"dst_page"`` (sorted by the page of each token's destination row, one more
+    small launch; measured net -1% to +1%, so off by default); None takes
+    :data:`DEFAULT_ORDER` for the element type.
     """
 
     def __init__(
@@ -433,6 +439,18 @@ class ShiftPlan:
         """K and V read once and written once: 2 * tokens * layers * heads * 2D * elem."""
         eb = self.dst.first.element_size()
         return 2 * self.tokens * self.dst.layers * self.dst.heads * 2 * self.dst.head_size * eb
+
+    @property
+    def metadata_bytes(self) -> dict:
+        """What a launch moves besides K and V, each counted once: the span table and
+        index arrays the kernels read, the per-span rotation tables, and (two-launch
+        path) the 32-byte token records the plan pass writes and the shift reads."""
+        idx = sum(d.src.index_len * (8 if d.src.mode == MODES["slots"] else 4)
+                  + d.dst.index_len * (8 if d.dst.mode == MODES["slots"] else 4)
+                  for d in self.descs[:1])
+        return {"spans": self.n_spans * _lib.SPAN_DTYPE.itemsize, "index": int(idx),
+                "tables": self.n_spans * 2 * self.rotary * 4,
+                "records": 0 if self.direct else 32 * self.tokens}
 
     def launch(self, stream: int | None = None, error_flags: torch.Tensor | None = None) -> None:
         """Enqueue the shift on ``stream`` (default: current): a plan launch and a shift
