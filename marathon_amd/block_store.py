@@ -141,6 +141,9 @@ class BlockShiftStore(StoreCore):
     def _has_layer(self, entry: _BlockEntry, layer: str) -> bool:
         return layer in entry.layers
 
+    def _has_layers(self, entry: _BlockEntry, layers) -> bool:
+        return entry.layers.issuperset(layers)
+
     def _held_tokens(self, entry: _BlockEntry) -> int:
         if self.truncate:
             return entry.size

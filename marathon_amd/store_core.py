@@ -98,6 +98,11 @@ class StoreCore:
     def _has_layer(self, entry, layer: str) -> bool:
         raise NotImplementedError
 
+    def _has_layers(self, entry, layers) -> bool:
+        """Whether every one of ``layers`` can be read (a fast path for the usual case;
+        False sends the caller through :meth:`_has_layer` one layer at a time)."""
+        return False
+
     def _held_tokens(self, entry) -> int:
         raise NotImplementedError
 
@@ -178,12 +183,15 @@ class StoreCore:
         if entry is None or not self._readable(entry, start, n):
             return next(iter(layers), None)
         missing = None
-        loaded = 0
-        for layer in layers:
-            if not self._has_layer(entry, layer):
-                missing = layer
-                break
-            loaded += 1
+        if self._has_layers(entry, layers):
+            loaded = len(layers)
+        else:
+            loaded = 0
+            for layer in layers:
+                if not self._has_layer(entry, layer):
+                    missing = layer
+                    break
+                loaded += 1
         if loaded:
             self.loaded_token_layers += n * loaded
             self._touch(session)  # the LRU order one touch per layer leaves
