@@ -517,7 +517,8 @@ def ceilings(dev, steps: int, warmup: int, stream) -> dict:
     * ``headline_identity_tables``: the headline shift through the same kernel, with the
       source block table and the destination slots made the identity, so every span is
       one contiguous run on each side.  The gap between this and the headline is what
-      scattered 64 KB blocks cost.
+      scattered 64 KB blocks cost.  ``headline_fp8_identity_tables``: the same for the
+      fp8 shift (32 KB blocks).
     """
     import numpy as np
     import torch
@@ -544,21 +545,24 @@ def ceilings(dev, steps: int, warmup: int, stream) -> dict:
     del a, b
     torch.cuda.empty_cache()
 
-    wl = W.qwen3_14b_multispan(dev)
-    wl.src_index = torch.arange(wl.src.first.shape[0], dtype=torch.int32)
-    wl.dst_index = torch.cat([torch.arange(int(r["dst_pos"]), int(r["dst_pos"]) + int(r["n_tokens"]),
-                                           dtype=torch.int64) for r in wl.spans])
-    if int(wl.dst_index.max()) >= wl.dst.first.shape[0] * 16:
-        raise AssertionError("identity slots exceed the destination cache")
-    plan = wl.plan()
-    warm_up(lambda: plan.launch(stream.cuda_stream))
-    _, per = time_plan(plan, max(steps, 50), warmup, stream)
-    ms = float(np.median(per))
-    gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
-    out["headline_identity_tables"] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
-                                       "frac_of_peak": round(gbs / PEAK_GBS, 4)}
-    del wl, plan
-    torch.cuda.empty_cache()
+    for name, make in (("headline_identity_tables", W.qwen3_14b_multispan),
+                       ("headline_fp8_identity_tables", W.qwen3_14b_multispan_fp8)):
+        wl = make(dev)
+        wl.src_index = torch.arange(wl.src.first.shape[0], dtype=torch.int32)
+        wl.dst_index = torch.cat([torch.arange(int(r["dst_pos"]),
+                                               int(r["dst_pos"]) + int(r["n_tokens"]),
+                                               dtype=torch.int64) for r in wl.spans])
+        if int(wl.dst_index.max()) >= wl.dst.first.shape[0] * 16:
+            raise AssertionError("identity slots exceed the destination cache")
+        plan = wl.plan()
+        warm_up(lambda: plan.launch(stream.cuda_stream))
+        _, per = time_plan(plan, max(steps, 50), warmup, stream)
+        ms = float(np.median(per))
+        gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+        out[name] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        del wl, plan
+        torch.cuda.empty_cache()
     return out
 
 

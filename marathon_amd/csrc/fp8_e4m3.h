@@ -6,17 +6,20 @@
 // callers rewrite NaN lanes to 0x7F.
 //
 // quant(): y / scale through Markstein's correction, q0 = RN(y * r),
-// q = fma(fma(-q0, scale, y), r, q0) with r = RN(1 / scale): three VALU operations where
-// the compiler's correctly rounded division takes about ten (measured 8% slower on the
-// fp8 Qwen3-14B shift).  Markstein's theorem makes q the correctly rounded quotient
-// whenever q0 is within one ulp of y / scale.  Checked exhaustively on the CPU: q equals
-// RN(y / scale) for every fp32 y with 2^-12 <= |y / scale| < 2^10 (the quotients that
-// can change an e4m3fn code) at every K scale of the fp8 workloads and GPU tests, and on
-// 3e8 random pairs with scales over 41 binades; other scales are checked only by that
-// random sample.  Smaller quotients encode to a signed zero either way, larger ones
-// clamp.  copysign keeps -0 / scale = -0.  The result is clamped to +-448 with IEEE
-// minNum/maxNum, which turn a NaN into 448: callers that can see NaN inputs rewrite
-// those bytes.
+// e = RN(q0 * scale - y), q = RN(-e * r + q0) with r = RN(1 / scale): three VALU
+// operations where the compiler's correctly rounded division takes about ten (measured
+// 8% slower on the fp8 Qwen3-14B shift).  -e is the usual residual RN(y - q0 * scale)
+// (rounding is symmetric), so q is Markstein's quotient, which his theorem makes the
+// correctly rounded one whenever q0 is within one ulp of y / scale.  Checked
+// exhaustively on the CPU: q equals RN(y / scale) for every fp32 y with
+// 2^-12 <= |y / scale| < 2^10 (the quotients that can change an e4m3fn code) at every
+// K scale of the fp8 workloads and GPU tests, and on 3e8 random pairs with scales over
+// 41 binades; other scales are checked only by that random sample.  Smaller quotients
+// encode to a signed zero either way, larger ones clamp.  Computing the residual with
+// its sign flipped also keeps the sign of a zero quotient: y = -0 gives e = +0 and
+// q = -0 + -0 = -0, y = +0 gives q = -0 + +0 = +0.  The result is clamped to +-448 by
+// one median-of-three; what it gives for a NaN does not matter, since callers that can
+// see NaN inputs rewrite those bytes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -41,15 +44,16 @@ __device__ __forceinline__ void decode4(uint32_t w, float* out) {
   out[3] = hi[1];
 }
 
+// q clamped to +-448 (one v_med3_f32; a NaN q gives some value, which callers rewrite).
 __device__ __forceinline__ float clamp448(float q) {
-  return __builtin_fmaxf(__builtin_fminf(q, 448.0f), -448.0f);
+  return __builtin_amdgcn_fmed3f(q, -448.0f, 448.0f);
 }
 
-// clamp(RN(y / scale)); rcp must be RN(1 / scale).
+// clamp(RN(y / scale)) for finite y; rcp must be RN(1 / scale).
 __device__ __forceinline__ float quant(float y, float scale, float rcp) {
   const float q0 = y * rcp;
-  const float r = __builtin_fmaf(-q0, scale, y);
-  return clamp448(__builtin_copysignf(__builtin_fmaf(r, rcp, q0), y));
+  const float e = __builtin_fmaf(q0, scale, -y);
+  return clamp448(__builtin_fmaf(-e, rcp, q0));
 }
 
 // Four in-range floats to four codes (round to nearest even), low byte first.

@@ -422,8 +422,10 @@ struct Rotor<MKV_F32> {
 };
 
 // fp8 e4m3fn: dequantise with the layer's K scale, rotate as above, requantise
-// (codec in fp8_e4m3.h).  Lanes whose inputs hold a NaN code recompute which outputs
-// are NaN and write the canonical 0x7F there.
+// (codec in fp8_e4m3.h).  When any lane of the wave holds a NaN code, every lane
+// recomputes which of its outputs are NaN and writes the canonical 0x7F there.  A lane's
+// partner chunk is another active lane's own chunk (the partner sits in the same row,
+// so it runs this code too), so one ballot over the lanes' own chunks covers both.
 template <>
 struct Rotor<MKV_FP8_E4M3> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
@@ -442,10 +444,9 @@ struct Rotor<MKV_FP8_E4M3> {
       }
       out[w] = encode4(q);
     }
-    const bool any_nan = has_nan_code(mine[0]) | has_nan_code(mine[1]) | has_nan_code(mine[2]) |
-                         has_nan_code(mine[3]) | has_nan_code(part[0]) | has_nan_code(part[1]) |
-                         has_nan_code(part[2]) | has_nan_code(part[3]);
-    if (__builtin_expect(any_nan, 0)) {
+    const bool own_nan = has_nan_code(mine[0]) || has_nan_code(mine[1]) ||
+                         has_nan_code(mine[2]) || has_nan_code(mine[3]);
+    if (__builtin_expect(__ballot(own_nan) != 0, 0)) {
       // y is NaN exactly when an input of its rotation is (every other input is finite)
 #pragma unroll
       for (int w = 0; w < 4; ++w) {

@@ -1,7 +1,8 @@
 /* Exhaustive check of the fp8 requantisation's division (CPU, test infrastructure).
  *
- * The shift kernel divides by the layer's K scale s with Markstein's correction:
- *   r = RN(1/s), q0 = RN(y*r), e = fma(-q0, s, y), q = fma(e, r, q0)
+ * The shift kernel divides by the layer's K scale s with Markstein's correction, its
+ * residual computed with the sign flipped (which keeps the sign of a zero quotient):
+ *   r = RN(1/s), q0 = RN(y*r), e = fma(q0, s, -y), q = fma(-e, r, q0)
  * and needs q == RN(y/s).  Markstein's theorem makes q correctly rounded whenever q0 is
  * within one ulp of y/s; rather than rely on that, this program walks, for each scale
  * given (as the hex bit pattern of the fp32 value), every fp32 y with
@@ -31,10 +32,13 @@ static uint32_t to_bits(float f) {
   return u;
 }
 
-static int markstein_ok(float y, float s, float r) {
+static float markstein(float y, float s, float r) {
   const float q0 = y * r;
-  const float q = fmaf(fmaf(-q0, s, y), r, q0);
-  return to_bits(q) == to_bits(y / s);
+  return fmaf(-fmaf(q0, s, -y), r, q0);
+}
+
+static int markstein_ok(float y, float s, float r) {
+  return to_bits(markstein(y, s, r)) == to_bits(y / s);
 }
 
 typedef struct {
@@ -100,6 +104,11 @@ int main(int argc, char** argv) {
       bad += jobs[t].bad;
       total += jobs[t].total;
     }
+    /* a zero quotient keeps the sign of y (-0 / s = -0) */
+    const float r = 1.0f / s;
+    bad += to_bits(markstein(0.0f, s, r)) != 0u;
+    bad += to_bits(markstein(-0.0f, s, r)) != 0x80000000u;
+    total += 2;
     printf("scale %a: %lld mismatches\n", s, bad);
     mismatches += bad;
   }
