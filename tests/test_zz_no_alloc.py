@@ -35,7 +35,7 @@ def _noalloc_desc(d: _lib.ShiftDesc) -> _lib.ShiftDesc:
     return out
 
 
-def _run_case(gpu, wl):
+def _run_case(gpu, wl, order="none"):
     L = _lib.lib()
     dst_b = CacheSet([[c.clone() for c in wl.dst.caches[0]]], "hnd", 16)
     want = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
@@ -43,10 +43,12 @@ def _run_case(gpu, wl):
     orc.shift_spans(oracle_spans(wl.spans), src_o, want, wl.inv_freq.numpy(),
                     dname(wl.dst.first.dtype),
                     None if wl.k_scale is None else wl.k_scale.numpy())
-    plan_a = wl.plan()
+    # the two-launch path (the direct path uses no workspace, so no scratch either)
+    plan_a = wl.plan(direct=False, order=order)
     plan_b = ShiftPlan(wl.spans, wl.src, dst_b, inv_freq=wl.inv_freq, src_mode=wl.src_mode,
                        src_index=wl.src_index, dst_mode=wl.dst_mode, dst_index=wl.dst_index,
-                       k_scale=wl.k_scale)
+                       k_scale=wl.k_scale, direct=False, order=order)
+    assert not plan_a.direct and not plan_b.direct
     torch.cuda.synchronize(gpu)  # both plans' tables have arrived
     stream = ctypes.c_void_p(current_stream(gpu))
     flags = torch.zeros(2, dtype=torch.int32, device=gpu)
@@ -66,17 +68,21 @@ def _run_case(gpu, wl):
         assert np.array_equal(a, want.caches[0][layer]), f"layer {layer}: differs from the oracle"
 
 
+@pytest.mark.parametrize("order", ["none", "dst_page"])
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
-def test_noalloc_matches_the_workspace_entry_point_twice(gpu, dtype):
+def test_noalloc_matches_the_workspace_entry_point_twice(gpu, dtype, order):
     for layers, history in ((3, 6144), (2, 1024)):  # the second call is smaller
-        print(f"case no-alloc {dtype} layers={layers} history={history}", flush=True)
+        print(f"case no-alloc {dtype} order={order} layers={layers} history={history}",
+              flush=True)
         if dtype == "bf16":
             wl = W.qwen3_14b_multispan(gpu, layers=layers, history=history, dst_fill="random")
         else:
             wl = W.qwen3_14b_multispan_fp8(gpu, layers=layers, history=history)
         need = _lib.lib().mkv_shift_workspace_size(wl.tokens, len(wl.spans), 128)
+        if order != "none":
+            need += 32 * wl.tokens + (1 << 20)  # MKV_ORDER_EXTRA_BYTES(total_tokens)
         assert 0 < need <= _lib.MKV_NOALLOC_SCRATCH_BYTES
-        _run_case(gpu, wl)
+        _run_case(gpu, wl, order)
         del wl
         torch.cuda.empty_cache()
 
