@@ -22,21 +22,32 @@ pytestmark = pytest.mark.gpu
 
 
 def _check_workload(wl, dev, dtype_name="bf16"):
+    """Every destination byte against the oracle, through the two-launch path and,
+    where eligible, the direct path (each run from the same starting caches)."""
+    before = [[t.clone() for t in row] for row in wl.dst.caches]
     src_o = oracle_side(wl.src, wl.src_mode, wl.src_index)
     dst_o = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
     k_scale = None if wl.k_scale is None else wl.k_scale.numpy()
     orc.shift_spans(oracle_spans(wl.spans), src_o, dst_o, wl.inv_freq.numpy(), dtype_name,
                     k_scale)
-    flags = torch.zeros(1, dtype=torch.int32, device=dev)
-    wl.plan().launch(error_flags=flags)
-    torch.cuda.synchronize(dev)
-    assert int(flags.item()) == 0
-    for g, row in enumerate(wl.dst.caches):
-        for layer, t in enumerate(row):
-            got = bits(t)
-            want = dst_o.caches[g][layer]
-            bad = int((got != want).sum())
-            assert bad == 0, f"group {g} layer {layer}: {bad} elements differ"
+    for direct in (False, True):
+        plan = wl.plan(direct=direct)
+        if direct and not plan.direct:
+            continue
+        for row, saved in zip(wl.dst.caches, before):
+            for t, b in zip(row, saved):
+                t.copy_(b)
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        plan.launch(error_flags=flags)
+        torch.cuda.synchronize(dev)
+        assert int(flags.item()) == 0, f"direct={plan.direct}"
+        for g, row in enumerate(wl.dst.caches):
+            for layer, t in enumerate(row):
+                got = bits(t)
+                want = dst_o.caches[g][layer]
+                bad = int((got != want).sum())
+                assert bad == 0, (f"direct={plan.direct} group {g} layer {layer}: "
+                                  f"{bad} elements differ")
 
 
 @pytest.mark.parametrize("history,layers", [(2048, 3), (4099, 2)])
@@ -123,7 +134,7 @@ def test_connector_loader_end_to_end(gpu):
 
 
 def _two_session_plan(gpu, dtype, heads, d, rotary, seed, spans, table, k_scale=None,
-                      fill=None):
+                      fill=None, direct=None):
     """Two flat sessions (300 and 200 rows) -> an HND paged cache addressed through a
     block table; returns (plan, dst caches)."""
     from marathon_amd.spans import CacheSet, ShiftPlan, span_array
@@ -138,7 +149,8 @@ def _two_session_plan(gpu, dtype, heads, d, rotary, seed, spans, table, k_scale=
           for _ in range(layers)]
     plan = ShiftPlan(span_array(spans), CacheSet(bufs, "flat"), CacheSet([kv], "hnd", bs),
                      inv_freq=inv_freq(rotary), src_mode="flat", dst_mode="table",
-                     dst_index=torch.tensor(table, dtype=torch.int32), k_scale=k_scale)
+                     dst_index=torch.tensor(table, dtype=torch.int32), k_scale=k_scale,
+                     direct=direct)
     return plan, kv
 
 
@@ -303,8 +315,9 @@ def test_batched_extreme_deltas_match_oracle(gpu, dtype):
         assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"layer {layer}"
 
 
+@pytest.mark.parametrize("direct", [False, None])
 @pytest.mark.parametrize("heads", [8, 2, 1])
-def test_out_of_range_rows_are_flagged_and_skipped(gpu, heads):
+def test_out_of_range_rows_are_flagged_and_skipped(gpu, heads, direct):
     """Bad indices on either side never write: a -1 and a too-large block id in the
     destination table, source positions past a session's rows, and a span naming a
     group that does not exist.  Each raises its flag; every other row lands exactly as
@@ -312,7 +325,7 @@ def test_out_of_range_rows_are_flagged_and_skipped(gpu, heads):
     several tokens per pass, good and bad ones side by side."""
     from marathon_amd import _lib
 
-    print(f"case out-of-range rows heads={heads}", flush=True)
+    print(f"case out-of-range rows heads={heads} direct={direct}", flush=True)
     table = torch.randperm(48, generator=torch.Generator().manual_seed(5)).tolist()
     bad_table = list(table)
     bad_table[2] = -1  # positions 32..47
@@ -326,9 +339,9 @@ def test_out_of_range_rows_are_flagged_and_skipped(gpu, heads):
                 (190, 400, 0, 0, 10, -5, 1, 0)]     # src 190..200
     fill = torch.full((48, heads, 16, 256), 3.0).to(torch.bfloat16)
     plan_b, kv_b = _two_session_plan(gpu, torch.bfloat16, heads, 128, 128, 4, spans_bad,
-                                     bad_table, fill=fill)
+                                     bad_table, fill=fill, direct=direct)
     plan_g, kv_g = _two_session_plan(gpu, torch.bfloat16, heads, 128, 128, 4, spans_ok, table,
-                                     fill=fill)
+                                     fill=fill, direct=direct)
     fb = torch.zeros(1, dtype=torch.int32, device=gpu)
     fg = torch.zeros(1, dtype=torch.int32, device=gpu)
     plan_b.launch(error_flags=fb)
