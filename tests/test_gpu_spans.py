@@ -639,20 +639,22 @@ def test_page_order_over_a_destination_wider_than_256_pages(gpu):
         assert np.array_equal(bits(kv[0]), dst_o.caches[0][0]), order
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float8_e4m3fn])
-@pytest.mark.parametrize("layers", [6, 9])
-def test_direct_path_above_the_wide_threshold(gpu, dtype, layers):
+@pytest.mark.parametrize("dtype,d,layers", [
+    (torch.bfloat16, 128, 6), (torch.bfloat16, 128, 9), (torch.float32, 128, 6),
+    (torch.float8_e4m3fn, 128, 9), (torch.float16, 64, 5), (torch.bfloat16, 256, 7),
+    (torch.float32, 256, 4)])
+def test_direct_path_above_the_wide_threshold(gpu, dtype, d, layers):
     """A direct shift of more than 2,560 (token, layer) rows: 2- and 4-byte elements move
-    four layers per workgroup, so 6 and 9 layers leave a partial last group (fp8 stays at
-    one layer per workgroup).  Every destination byte against the oracle."""
+    four layers per workgroup, so 5, 6, 7 and 9 layers leave a partial last group (fp8
+    stays at one layer per workgroup).  Every destination byte against the oracle."""
     from marathon_amd.spans import CacheSet, ShiftPlan
 
     eb = torch.empty(0, dtype=dtype).element_size()
-    heads = 64 // (128 * eb // 16)  # the smallest head count the direct path takes
-    print(f"case wide direct shift {dtype} heads={heads} layers={layers}", flush=True)
+    heads = max(1, 64 // (d * eb // 16))  # the smallest head count the direct path takes
+    print(f"case wide direct shift {dtype} d={d} heads={heads} layers={layers}", flush=True)
     rng = np.random.default_rng(layers)
     g = torch.Generator().manual_seed(layers)
-    d, bs, hist, blocks = 128, 16, 1200, 120
+    bs, hist, blocks = 16, 1200, 120
     k_scale = None
     if dtype == torch.float8_e4m3fn:
         k_scale = torch.from_numpy(rng.uniform(0.01, 0.1, layers).astype(np.float32))
@@ -665,12 +667,13 @@ def test_direct_path_above_the_wide_threshold(gpu, dtype, layers):
             (900, 0, 0, 550, 150, 0, 0, 0)]
     assert n * layers > 2560
     src_set, dst_set = CacheSet([src], "flat"), CacheSet([kv], "hnd", bs)
-    plan = ShiftPlan(span_array(rows), src_set, dst_set, inv_freq=inv_freq(), src_mode="flat",
+    inv = inv_freq(d)
+    plan = ShiftPlan(span_array(rows), src_set, dst_set, inv_freq=inv, src_mode="flat",
                      dst_mode="slots", dst_index=dst_slots, k_scale=k_scale, direct=True)
     assert plan.direct
     src_o = oracle_side(src_set, "flat", None)
     dst_o = oracle_side(dst_set, "slots", dst_slots)
-    orc.shift_spans(oracle_spans(span_array(rows)), src_o, dst_o, inv_freq().numpy(),
+    orc.shift_spans(oracle_spans(span_array(rows)), src_o, dst_o, inv.numpy(),
                     dname(dtype), None if k_scale is None else k_scale.numpy())
     flags = torch.zeros(1, dtype=torch.int32, device=gpu)
     plan.launch(error_flags=flags)
