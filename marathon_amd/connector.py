@@ -5,8 +5,9 @@ for every load of a step and every layer, ``ShiftStore.read`` and one
 ``scatter_shifted`` launch (:481-534, loop at :505-518): 40 launches per load on
 Qwen3-14B, plus per-layer Python.  :class:`ShiftLoader` keeps the same inputs -- the
 ``_Load`` list (:135-140), the registered paged caches (:393-412) and the session store
--- and issues the whole step as one batched launch (:class:`marathon_amd.spans.ShiftPlan`):
-every load x every layer, sources read straight out of each session's store buffer.
+-- and issues the whole step as one batched shift (:class:`marathon_amd.spans.ShiftPlan`,
+or :class:`marathon_amd.spans.SmallShifts` for a short step): every load x every layer,
+sources read straight out of each session's store buffer.
 
 Also here, as host logic: the layout detection of ``register_kv_caches`` (:393-402) and
 the multi-segment block alignment of ``_accept_multi`` (:225-245).
@@ -14,9 +15,9 @@ the multi-segment block alignment of ``_accept_multi`` (:225-245).
 Slots on the device.  The reference's scheduler builds every load's and save's int64
 slot list on the host (``slots()``, :349-366 / :320) and the worker copies it H2D
 (:504): 8 bytes per token.  A :class:`Load` or :class:`Save` built with ``from_blocks``
-carries the request's block table and a position range instead.  The kernel's plan pass
-turns positions into slots on the device (``MKV_ADDR_TABLE``), so the host ships 4
-bytes per 16 tokens.  Either store works as the source or target: the reference's flat
+carries the request's block table and a position range instead.  The kernels turn
+positions into slots on the device (``MKV_ADDR_TABLE``), so the host ships 4 bytes per
+16 tokens.  Either store works as the source or target: the reference's flat
 :class:`~marathon_amd.shift_store.ShiftStore`, or the
 :class:`~marathon_amd.block_store.BlockShiftStore` pool, read and written through its
 block tables.
