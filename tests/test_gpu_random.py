@@ -1,12 +1,14 @@
 """Seeded random batched shifts against the oracle, byte for byte.
 
 Each case draws:
-* a geometry: element type, head size, heads, rotary width, layers, block size;
+* a geometry: element type, head size, heads, rotary width, one to five layers, block
+  size;
 * a source side: flat session stores, or paged NHD / HND caches through block tables,
   in one to three groups;
 * a destination side: a paged NHD or HND cache through a slot mapping or a block table,
   or flat session stores, in one or two groups;
-* one to six spans with disjoint destinations and deltas of both signs, zero and large.
+* one to six spans of up to 240 tokens, with disjoint destinations and deltas of both
+  signs, zero and large (the largest cases pass the direct path's four-layer threshold).
 Every destination byte of every layer must equal the oracle's, and no error flag may be
 raised.
 """
@@ -39,7 +41,7 @@ def _case(seed: int):
     rot_choices = [r for r in (0, d // 2, d) if r % (2 * per_chunk) == 0]
     rotary = int(rng.choice(rot_choices))
     heads = int(rng.choice([1, 2, 3, 4, 5, 6, 8, 12, 16]))
-    layers = int(rng.integers(1, 4))
+    layers = int(rng.integers(1, 6))
     bs = int(rng.choice([16, 16, 32]))
     src_layout = str(rng.choice(["flat", "nhd", "hnd"]))
     dst_layout = str(rng.choice(["nhd", "hnd", "flat"]))
@@ -86,7 +88,7 @@ def _build(c, gpu):
     raw = []
     for _ in range(n_spans):
         g = int(rng.integers(c["src_groups"]))
-        n = int(rng.integers(1, min(120, src_rows[g]) + 1))
+        n = int(rng.integers(1, min(240, src_rows[g]) + 1))
         sp = int(rng.integers(0, src_rows[g] - n + 1))
         dg = int(rng.integers(c["dst_groups"]))
         dp = dst_pos_space[dg] + int(rng.integers(0, 40))
