@@ -93,6 +93,12 @@
 #ifndef MKV_STORE_CPOL
 #define MKV_STORE_CPOL 18
 #endif
+// Cache policy of the data loads where the source row is wave-uniform: >= 0 loads
+// through a buffer resource with these policy bits; -1 global loads (non-temporal
+// with MKV_NT_LOAD).
+#ifndef MKV_LOAD_CPOL
+#define MKV_LOAD_CPOL -1
+#endif
 // Layers one workgroup moves (grid.y = ceil(layers / this)), each pass's token metadata
 // resolved once for all of them.  The direct path moves MKV_DIRECT_WIDE_LAYERS layers per
 // workgroup when a shift of 2- or 4-byte elements has more than MKV_DIRECT_WIDE_MIN_ROWS
@@ -312,6 +318,20 @@ __device__ __forceinline__ void store16_at(char* base, uint32_t lane_off, u32x4 
   __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(lane_off), 0, MKV_STORE_CPOL);
 #else
   store16(base + lane_off, v);
+#endif
+}
+
+// Load from a wave-uniform source row `base` at a per-lane 32-bit offset, with the
+// cache policy MKV_LOAD_CPOL (same bits as the stores).
+__device__ __forceinline__ u32x4 load16_at(const char* base, uint32_t lane_off) {
+#if MKV_LOAD_CPOL >= 0
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(base), 0, kRsrcRange, kRsrcWord3);
+  return __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(lane_off), 0,
+                                                   MKV_LOAD_CPOL));
+#else
+  return load16(base + lane_off);
 #endif
 }
 
@@ -1123,8 +1143,13 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
       kd[x] = u32x4{0, 0, 0, 0};
       vd[x] = u32x4{0, 0, 0, 0};
       if (xl[x] && lane_live) {
-        kd[x] = load16(sbk[x] + s_at[u] + s_lane);
-        vd[x] = load16(sbv[x] + s_at[u] + s_lane);
+        if constexpr (UNIFORM) {
+          kd[x] = load16_at(sbk[x] + s_at[u], s_lane);
+          vd[x] = load16_at(sbv[x] + s_at[u], s_lane);
+        } else {
+          kd[x] = load16(sbk[x] + s_at[u] + s_lane);
+          vd[x] = load16(sbv[x] + s_at[u] + s_lane);
+        }
       }
     }
 #if MKV_TABLE_WITH_DATA
