@@ -519,6 +519,10 @@ def ceilings(dev, steps: int, warmup: int, stream) -> dict:
       one contiguous run on each side.  The gap between this and the headline is what
       scattered 64 KB blocks cost.  ``headline_fp8_identity_tables``: the same for the
       fp8 shift (32 KB blocks).
+    * ``headline_zero_delta`` / ``headline_fp8_zero_delta``: the headline shift (shuffled
+      tables) with every span's delta set to 0, so K is copied like V: the same gather and
+      scatter with no rotation.  The gap between this and the headline is what the
+      rotation costs.
     """
     import numpy as np
     import torch
@@ -554,6 +558,20 @@ def ceilings(dev, steps: int, warmup: int, stream) -> dict:
                                                dtype=torch.int64) for r in wl.spans])
         if int(wl.dst_index.max()) >= wl.dst.first.shape[0] * 16:
             raise AssertionError("identity slots exceed the destination cache")
+        plan = wl.plan()
+        warm_up(lambda: plan.launch(stream.cuda_stream))
+        _, per = time_plan(plan, max(steps, 50), warmup, stream)
+        ms = float(np.median(per))
+        gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+        out[name] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        del wl, plan
+        torch.cuda.empty_cache()
+
+    for name, make in (("headline_zero_delta", W.qwen3_14b_multispan),
+                       ("headline_fp8_zero_delta", W.qwen3_14b_multispan_fp8)):
+        wl = make(dev)
+        wl.spans["delta"] = 0
         plan = wl.plan()
         warm_up(lambda: plan.launch(stream.cuda_stream))
         _, per = time_plan(plan, max(steps, 50), warmup, stream)
