@@ -3,8 +3,9 @@
 Workload (one "step" = one whole shift, one launch): the Qwen3-14B-shaped multi-span
 shift -- 40 layers, 8 KV heads, head_dim 128, bf16, a 30,720-token history with 8
 reused spans (seed 3: 22,141 tokens, deltas in [-2048, 2048] incl. 0, no boundary on a
-multiple of 16), read from the session store's block layout through a shuffled block
-table and written into an HND paged cache through a slot mapping.  Inputs are resident
+multiple of 16), read from the session store's block layout (each 16-token block a K
+plane then a V plane, as the block store holds it) through a shuffled block table and
+written into an HND paged cache through a slot mapping.  Inputs are resident
 in HBM before timing.  Bytes are algorithmic: each K and V element read once and
 written once (2 * tokens * layers * 8 * 256 * 2 B), reported in decimal GB/s.
 
@@ -31,6 +32,8 @@ Prints one JSON line.  Also measured, in the same line:
   block tables made the identity: what the GPU streams with nothing scattered.
 * ``dst_layouts``: the headline shift into fused NHD caches and into caches that keep K
   and V in separate planes, beside the fused HND headline.
+* ``src_layouts``: the headline shift, bf16 and fp8, from the store's K/V planes and
+  from store blocks whose rows hold K then V per head.
 * ``connector_step`` / ``save_step``: the connector's load and save calls end to end.
 * ``plan_variants``: A/B of the token records' order (span order against destination
   page order) and of the single-launch direct path against the two-launch path.
@@ -121,7 +124,7 @@ def spot_check(wl, rows: int = 96, seed: int = 0) -> int:
         sblk, soff = int(src_tab[pos // 16]), pos % 16
         slot = int(dst_slots[int(sp["dst_index"]) + i])
         dblk, doff = slot // 16, slot % 16
-        src_row = wl.src.caches[0][layer][sblk, soff].cpu()  # NHD: [heads, 2D]
+        src_row = wl.src.fused(0, layer, (sblk, soff)).cpu()  # [heads, 2D], K then V
         got = wl.dst.caches[0][layer][dblk, :, doff].cpu()  # HND: [heads, 2D]
         sb = src_row.view(torch.int16).numpy().view(np.uint16)
         gb = got.view(torch.int16).numpy().view(np.uint16)
@@ -629,6 +632,32 @@ def dst_layouts(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def src_layouts(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: the headline shift (bf16 and fp8) from each block layout of the
+    session store -- K and V planes per block, ``[blocks, 2, 16, heads, D]``, and rows of
+    K then V per head, ``[blocks, 16, heads, 2D]`` -- the same values, blocks and tables;
+    the two launches alternate over 5 rounds (the best round's median of each).  The
+    block store keeps planes for 2- and 4-byte elements and rows for fp8."""
+    import torch
+
+    from marathon_amd import workloads as W
+
+    out = {}
+    for dt, make in (("bf16", W.qwen3_14b_multispan), ("fp8", W.qwen3_14b_multispan_fp8)):
+        wls = {layout: make(dev, src_layout=layout) for layout in ("planes", "fused")}
+        plans = {layout: wl.plan() for layout, wl in wls.items()}
+        for plan in plans.values():
+            warm_up(lambda: plan.launch(stream.cuda_stream))
+        best = _ab(plans, max(steps, 50), warmup, stream, rounds=5)
+        for layout, ms in best.items():
+            gbs = plans[layout].algorithmic_bytes / (ms / 1e3) / 1e9
+            out[f"{layout}_{dt}"] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
+                                     "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        del wls, plans
+        torch.cuda.empty_cache()
+    return out
+
+
 def _same_output(a_plan, b_plan, caches) -> bool:
     """Run two plans of one workload into zeroed caches; whether every byte matches."""
     import torch
@@ -960,6 +989,8 @@ def main() -> int:
                     help="skip the plain elementwise copy and the identity-table headline")
     ap.add_argument("--no-dst-layouts", action="store_true",
                     help="skip the headline shift into the other paged-cache layouts")
+    ap.add_argument("--no-src-layouts", action="store_true",
+                    help="skip the headline shift from the store's other block layout")
     ap.add_argument("--no-connector-step", action="store_true",
                     help="skip the end-to-end connector load and save step timings")
     ap.add_argument("--no-plan-variants", action="store_true",
@@ -974,8 +1005,8 @@ def main() -> int:
     if args.only:
         keep = {x.strip() for x in args.only.split(",") if x.strip()}
         sections = {"reference_shape", "reference_loop", "other_workloads", "tp_shares",
-                    "size_sweep", "ceilings", "dst_layouts", "connector_step",
-                    "plan_variants", "cpu_baseline"}
+                    "size_sweep", "ceilings", "dst_layouts", "src_layouts",
+                    "connector_step", "plan_variants", "cpu_baseline"}
         if keep - sections - {"headline"}:  # "headline": the headline line alone
             ap.error(f"--only: unknown sections {sorted(keep - sections)}")
         for name in sections - keep:
@@ -1053,6 +1084,9 @@ def main() -> int:
     if not args.no_dst_layouts:
         log("destination layouts (fused HND / NHD, split K/V planes)")
         extra["dst_layouts"] = dst_layouts(dev, side_steps, args.warmup, stream)
+    if not args.no_src_layouts:
+        log("store block layouts (K/V planes, fused rows), bf16 and fp8")
+        extra["src_layouts"] = src_layouts(dev, side_steps, args.warmup, stream)
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
         extra["connector_step"] = connector_step(dev, side_steps, args.warmup)

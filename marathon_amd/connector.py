@@ -409,10 +409,11 @@ class ShiftLoader:
         dst_mode, dst_index, dst_rows = paged_index(taken, self.block_size)
         rows = []
         if blocky:
-            # one pool per layer; each load's window of its session's block table is
-            # the source index
-            src = self._sets.get("store", [self.store.pools(names)], "nhd",
-                                 self.store.block_size)
+            # one pool per layer (K and V planes, or fused rows); each load's window of
+            # its session's block table is the source index
+            caches, v_caches = self.store.kernel_views(names)
+            src = self._sets.get("store", [caches], "nhd", self.store.block_size,
+                                 v_caches=None if v_caches is None else [v_caches])
             src_mode = "table"
             src_index, src_rows = _store_windows(self.store, taken, lambda ld: ld.src_start)
             for load, (spos, sidx), (dpos, didx) in zip(taken, src_rows, dst_rows):
@@ -473,11 +474,7 @@ class ShiftLoader:
         """``[n, heads, 2D]`` rows the load read, without the store's read accounting."""
         n = load.n
         if isinstance(self.store, BlockShiftStore):
-            pool = self.store.pool(name)
-            pos = torch.arange(load.src_start, load.src_start + n)
-            tab = torch.from_numpy(self.store.table(load.session).astype(np.int64))
-            bs = self.store.block_size
-            return pool[tab[pos // bs].to(pool.device), (pos % bs).to(pool.device)]
+            return self.store.gather(load.session, name, load.src_start, n)
         return self.store.buffer(load.session, name)[load.src_start:load.src_start + n]
 
     def _verify(self, name: str, load: Load, k_scale, layer: int) -> None:
@@ -755,8 +752,9 @@ class ShiftSaver:
         src_mode, src_index, src_rows = paged_index(taken, self.block_size)
         rows = []
         if blocky:
-            dst = self._sets.get("store", [self.store.pools(names)], "nhd",
-                                 self.store.block_size)
+            caches, v_caches = self.store.kernel_views(names)
+            dst = self._sets.get("store", [caches], "nhd", self.store.block_size,
+                                 v_caches=None if v_caches is None else [v_caches])
             dst_mode = "table"
             dst_index, dst_rows = _store_windows(self.store, taken, lambda sv: sv.dst_start)
             for sv, (spos, sidx), (dpos, didx) in zip(taken, src_rows, dst_rows):

@@ -151,6 +151,18 @@ class CacheSet:
     def head_size(self) -> int:
         return self.first.shape[-1] if self.split else self.first.shape[-1] // 2
 
+    def fused(self, group: int, layer: int, index=None) -> torch.Tensor:
+        """Rows of the (group, layer) cache with K and V side by side, ``[..., 2D]``:
+        ``cache[index]`` (the whole cache when ``index`` is None), and with split planes
+        a copy that puts the V plane's rows after the K plane's."""
+        k = self.caches[group][layer]
+        if index is not None:
+            k = k[index]
+        if not self.split:
+            return k
+        v = self.v_caches[group][layer]
+        return torch.cat((k, v if index is None else v[index]), dim=-1)
+
     @property
     def strides(self) -> tuple[int, int, int]:
         s = self.first.stride()

@@ -16,9 +16,12 @@ on the device from seeded generators.
 5. 32 sessions x 36 layers, histories in [2048, 32768], 1..6 spans per session,
    deltas in [-4096, 4096], one span table, one shared paged destination.
 
-The source is the session store in block layout (NHD blocks, read through a block
-table); the destination is an HND paged cache written through a slot mapping
-(workloads 2-4) or through per-request block tables (workload 5).
+The source is the session store in block layout (read through a block table), as
+:class:`~marathon_amd.block_store.BlockShiftStore` holds it for the element type
+(``store_layout``): bf16 blocks as a K plane then a V plane, ``[blocks, 2, 16, heads,
+D]``; fp8 blocks as rows of K then V per head, ``[blocks, 16, heads, 2D]``.
+``src_layout`` picks either for any type.  The destination is an HND paged cache written through a slot mapping (workloads 2-4) or
+through per-request block tables (workload 5).
 """
 
 from __future__ import annotations
@@ -29,6 +32,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .block_store import store_layout
 from .shift_kernels import inv_freq_for
 from .shift_store import slots as slot_map
 from .spans import CacheSet, ShiftPlan
@@ -196,6 +200,36 @@ def _paged(blocks, layout, heads=HEADS):
     return (blocks, heads, BLOCK, 2 * HEAD_SIZE) if layout == "hnd" else (blocks, BLOCK, heads, 2 * HEAD_SIZE)
 
 
+#: Block layouts of a session store: ``"planes"`` -- a K plane then a V plane per
+#: block, ``[blocks, 2, 16, heads, D]`` (the block store's pool); ``"fused"`` -- rows of
+#: K then V per head, ``[blocks, 16, heads, 2D]``.
+STORE_LAYOUTS = ("planes", "fused")
+
+
+def store_blocks(blocks: int, heads: int, dtype, gen, device, k_scale=None, v_scale=None,
+                 layout: str = "planes") -> torch.Tensor:
+    """One layer of a session store: ``blocks`` blocks of N(0, 1) K and V (fp8: divided
+    by the layer's K and V scales) in ``layout``."""
+    if layout not in STORE_LAYOUTS:
+        raise ValueError(f"store layout {layout!r}")
+    plane = (blocks, BLOCK, heads, HEAD_SIZE)
+    if dtype != torch.float8_e4m3fn:
+        if layout == "planes":
+            return _randn_cache((blocks, 2, BLOCK, heads, HEAD_SIZE), dtype, gen, device)
+        return _randn_cache(_paged(blocks, "nhd", heads), dtype, gen, device)
+    k = _randn_cache(plane, dtype, gen, device, k_scale)
+    v = _randn_cache(plane, dtype, gen, device, v_scale)
+    return torch.stack((k, v), dim=1) if layout == "planes" else torch.cat((k, v), dim=-1)
+
+
+def store_cache_set(groups: list, layout: str = "planes") -> CacheSet:
+    """A :class:`CacheSet` over ``groups[group][layer]`` tensors from :func:`store_blocks`."""
+    if layout == "planes":
+        return CacheSet([[t[:, 0] for t in row] for row in groups], "nhd", BLOCK,
+                        v_caches=[[t[:, 1] for t in row] for row in groups])
+    return CacheSet(groups, "nhd", BLOCK)
+
+
 def single_session_workload(
     name: str,
     layout: SpanLayout,
@@ -208,10 +242,14 @@ def single_session_workload(
     spare_blocks: int = 64,
     dst_fill: str = "zeros",
     heads: int = HEADS,
+    src_layout: str | None = None,
 ) -> Workload:
-    """One session's store (NHD blocks via a shuffled table) -> one HND paged cache via
-    a slot mapping: the single-span and multi-span workloads, bf16 or fp8.  ``heads``
-    below 8 is one GPU's share of the KV heads under tensor parallelism."""
+    """One session's store (blocks in ``src_layout``, via a shuffled table) -> one HND
+    paged cache via a slot mapping: the single-span and multi-span workloads, bf16 or
+    fp8.  ``heads`` below 8 is one GPU's share of the KV heads under tensor
+    parallelism.  ``src_layout``: ``"planes"`` or ``"fused"`` (default: the block store's
+    layout for ``dtype``)."""
+    src_layout = src_layout or store_layout(dtype)
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -226,14 +264,10 @@ def single_session_workload(
         k_scale, v_scale = torch.from_numpy(k), torch.from_numpy(v)
     src_caches, dst_caches = [], []
     for layer in range(layers):
-        if dtype == torch.float8_e4m3fn:
-            kk = _randn_cache(_paged(src_blocks, "nhd", heads)[:-1] + (HEAD_SIZE,), dtype, gen,
-                              device, k_scale[layer])
-            vv = _randn_cache(_paged(src_blocks, "nhd", heads)[:-1] + (HEAD_SIZE,), dtype, gen,
-                              device, v_scale[layer])
-            src_caches.append(torch.cat((kk, vv), dim=-1))
-        else:
-            src_caches.append(_randn_cache(_paged(src_blocks, "nhd", heads), dtype, gen, device))
+        fp8 = dtype == torch.float8_e4m3fn
+        src_caches.append(store_blocks(src_blocks, heads, dtype, gen, device,
+                                       k_scale[layer] if fp8 else None,
+                                       v_scale[layer] if fp8 else None, src_layout))
         if dst_fill == "random" and dtype != torch.float8_e4m3fn:
             dst_caches.append(_randn_cache(_paged(dst_pool, "hnd", heads), dtype, gen, device))
         else:
@@ -248,7 +282,7 @@ def single_session_workload(
     return Workload(
         name,
         spans,
-        CacheSet([src_caches], "nhd", BLOCK),
+        store_cache_set([src_caches], src_layout),
         CacheSet([dst_caches], "hnd", BLOCK),
         "table",
         torch.from_numpy(src_table),
@@ -310,7 +344,8 @@ def batched_sessions(device, layers: int = 36, seed: int = 5, sessions: int = 32
         nb = -(-lay.src_history // BLOCK)
         src_tables.append(rng.permutation(nb).astype(np.int32))
         dst_tables.append(perm[d_off : d_off + dst_need[g]])
-        src_caches.append([_randn_cache(_paged(nb, "nhd"), dtype, gen, device)
+        src_caches.append([store_blocks(nb, HEADS, dtype, gen, device,
+                                        layout=store_layout(dtype))
                            for _ in range(layers)])
         for s, d, n, dl in zip(lay.src_start, lay.dst_start, lay.length, lay.delta):
             rows.append((int(s), int(d), s_off, d_off, int(n), int(dl), g, 0))
@@ -321,7 +356,7 @@ def batched_sessions(device, layers: int = 36, seed: int = 5, sessions: int = 32
     return Workload(
         "batched restore",
         np.array(rows, dtype=_lib.SPAN_DTYPE),
-        CacheSet(src_caches, "nhd", BLOCK),
+        store_cache_set(src_caches, store_layout(dtype)),
         CacheSet([dst_caches], "hnd", BLOCK),
         "table",
         torch.from_numpy(np.concatenate(src_tables)),

@@ -38,8 +38,10 @@ def randn(shape, dtype, gen, scale: float = 1.0) -> torch.Tensor:
 
 
 def oracle_side(cs, mode: str, index) -> orc.Side:
-    """An oracle Side holding CPU bit copies of a marathon_amd CacheSet."""
-    caches = [[bits(t) for t in row] for row in cs.caches]
+    """An oracle Side holding CPU bit copies of a marathon_amd CacheSet (split K and V
+    planes as fused rows, K then V: the oracle's row format)."""
+    caches = [[bits(cs.fused(g, layer)) for layer in range(cs.layers)]
+              for g in range(cs.groups)]
     idx = None if index is None else index.detach().cpu().numpy()
     return orc.Side(caches, cs.layout, cs.block_size, mode, idx)
 

@@ -12,6 +12,7 @@
 from __future__ import annotations
 
 import numpy as np
+import pytest
 import torch
 
 from marathon_amd.block_store import BlockShiftStore
@@ -263,3 +264,43 @@ def test_lookup_layers_matches_per_layer_lookups():
             assert miss_a == miss_b
             assert a.stats() == b.stats()
             assert list(a._sessions) == list(b._sessions)
+
+
+def test_pool_holds_each_block_as_a_k_plane_then_a_v_plane():
+    """Rows written as [heads, 2D] land as K and V planes of their blocks; the planes are
+    views of the pool, reused while no pool changes; reads give the rows back."""
+    st = _store()
+    st.reserve("a", 0, 40)
+    rows = torch.arange(40 * 3 * 8, dtype=torch.float32).reshape(40, 3, 8)
+    st.write("a", "l0", 0, rows)
+    pool, tab = st.pool("l0"), st.table("a")
+    assert pool.shape == (st.pool_blocks, 2, 16, 3, 4)
+    for pos in (0, 15, 16, 39):
+        blk, off = int(tab[pos // 16]), pos % 16
+        assert torch.equal(pool[blk, 0, off], rows[pos, :, :4])
+        assert torch.equal(pool[blk, 1, off], rows[pos, :, 4:])
+    k, v = st.kernel_views(["l0"])
+    assert k[0].data_ptr() == pool.data_ptr() and v[0].data_ptr() == pool[:, 1].data_ptr()
+    assert k[0].shape == v[0].shape == (st.pool_blocks, 16, 3, 4)
+    assert st.kernel_views(["l0"])[0] is k  # the same lists while no pool changes
+    assert torch.equal(st.read("a", "l0", 3, 30), rows[3:33])
+    with pytest.raises(ValueError, match="K and V halves"):
+        st.write("a", "l1", 0, torch.zeros(40, 3, 7))
+
+
+def test_one_byte_elements_keep_fused_rows():
+    """fp8 pools hold rows of K then V per head; the kernels see them as fused caches."""
+    st = _store()
+    st.reserve("a", 0, 40)
+    rows = torch.randn(40, 2, 8).to(torch.float8_e4m3fn)
+    st.write("a", "l0", 0, rows)
+    pool, tab = st.pool("l0"), st.table("a")
+    assert pool.shape == (st.pool_blocks, 16, 2, 8)
+    assert torch.equal(pool[int(tab[1]), 3].view(torch.uint8), rows[19].view(torch.uint8))
+    caches, v_caches = st.kernel_views(["l0"])
+    assert caches[0] is pool and v_caches is None
+    assert torch.equal(st.read("a", "l0", 0, 40).view(torch.uint8), rows.view(torch.uint8))
+    st.reserve("a", 0, 40)
+    st.write("a", "l1", 0, torch.zeros(40, 2, 8))  # a float32 layer: planes
+    with pytest.raises(ValueError, match="mix block layouts"):
+        st.kernel_views(["l0", "l1"])

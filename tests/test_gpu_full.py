@@ -28,13 +28,12 @@ D = 128
 
 
 def _src_rows(wl, g, layer, sp):
-    """[n, heads, 2D] source rows of span ``sp`` (store block layout, NHD)."""
-    cache = wl.src.caches[g][layer]
+    """[n, heads, 2D] source rows of span ``sp`` (store blocks, K then V)."""
+    dev = wl.src.first.device
     pos = torch.arange(int(sp["src_pos"]), int(sp["src_pos"]) + int(sp["n_tokens"]),
-                       device=cache.device)
-    tab = wl.src_index.to(cache.device, torch.int64)[int(sp["src_index"]):]
-    blk = tab[pos // 16]
-    return cache[blk, pos % 16]
+                       device=dev)
+    tab = wl.src_index.to(dev, torch.int64)[int(sp["src_index"]):]
+    return wl.src.fused(g, layer, (tab[pos // 16], pos % 16))
 
 
 def _layer_rows(wl, layer, spans, src_slots, dst_slots):
@@ -43,9 +42,8 @@ def _layer_rows(wl, layer, spans, src_slots, dst_slots):
     dev = wl.dst.first.device
     src_parts, dst_parts = [], []
     for sp, ss, ds in zip(spans, src_slots, dst_slots):
-        cache = wl.src.caches[int(sp["src_group"])][layer]
         s = torch.from_numpy(ss).to(dev)
-        src_parts.append(cache[s // 16, s % 16])  # NHD store blocks
+        src_parts.append(wl.src.fused(int(sp["src_group"]), layer, (s // 16, s % 16)))
         d = torch.from_numpy(ds).to(dev)
         dst_parts.append(wl.dst.caches[int(sp["dst_group"])][layer][d // 16, :, d % 16])  # HND
     return torch.cat(src_parts), torch.cat(dst_parts)
@@ -161,13 +159,16 @@ def test_round_trip_at_full_size(gpu):
     print("case round trip (Qwen3-14B multi-span layout, 40 layers)", flush=True)
     wl = W.qwen3_14b_multispan(gpu)
     wl.plan().launch()
-    back = [torch.zeros_like(c) for c in wl.src.caches[0]]
+    first = wl.src.first  # a K plane, [blocks, 16, heads, D]
+    back = W.store_cache_set([[torch.zeros(first.shape[0], 2, *first.shape[1:],
+                                           dtype=first.dtype, device=gpu)
+                               for _ in range(wl.layers)]])
     # the way back: read the destination cache through the same slots, write a fresh
     # store in block layout through the source block table, rotate by -delta
     rows = [(0, int(sp["src_pos"]), int(sp["dst_index"]), int(sp["src_index"]),
              int(sp["n_tokens"]), -int(sp["delta"]), 0, 0) for sp in wl.spans]
     plan = ShiftPlan(span_array(rows), CacheSet([wl.dst.caches[0]], "hnd", 16),
-                     CacheSet([back], "nhd", 16), inv_freq=wl.inv_freq, src_mode="slots",
+                     back, inv_freq=wl.inv_freq, src_mode="slots",
                      src_index=wl.dst_index, dst_mode="table", dst_index=wl.src_index)
     plan.launch()
     torch.cuda.synchronize(gpu)
@@ -177,7 +178,7 @@ def test_round_trip_at_full_size(gpu):
                            device=gpu)
         for layer in range(0, wl.layers, 7):
             orig = _src_rows(wl, 0, layer, sp).float()
-            got = back[layer][tab[pos // 16], pos % 16].float()
+            got = back.fused(0, layer, (tab[pos // 16], pos % 16)).float()
             assert torch.equal(got[..., D:], orig[..., D:])
             k0 = orig[..., :D]
             pair = torch.maximum(k0.abs(), torch.roll(k0, D // 2, -1).abs())

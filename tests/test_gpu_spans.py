@@ -422,7 +422,7 @@ def test_plan_launch_replays_from_a_hip_graph(gpu, direct):
     with torch.cuda.graph(graph):
         plan.launch(error_flags=flags)
     for i in range(3):
-        for c in wl.src.caches[0]:
+        for c in wl.src.caches[0] + (wl.src.v_caches[0] if wl.src.split else []):
             c.mul_(-1.0 if i % 2 == 0 else 0.5)  # exact in bf16: a sign flip, a halving
         for c in wl.dst.caches[0]:
             c.zero_()
@@ -487,7 +487,7 @@ def test_load_read_back_check(gpu):
     assert store.reserve("s", 0, 500)
     for name in names:
         store.write_target("s", name, 0, 500, (heads, 2 * d), torch.bfloat16,
-                           gpu).copy_(torch.randn(store.pool_blocks, bs, heads, 2 * d,
+                           gpu).copy_(torch.randn(store.pool_blocks, 2, bs, heads, d,
                                                   generator=g).to(torch.bfloat16))
     kv = {name: torch.zeros(48, heads, bs, 2 * d, dtype=torch.bfloat16, device=gpu)
           for name in names}

@@ -75,8 +75,10 @@ class FingerprintWorker:
             # the worker's reserve mirrors the scheduler's (vllm_shift_connector.py:546-553)
             assert self.store.reserve(sv.session, sv.dst_start, sv.n)
             vals = [self.paged[s] for s in self._slots(sv, sv.dst_start)]
+            # rows [heads=1, 2D=2]: the token's fingerprint as its K and its V
             self.store.write(sv.session, "L0", sv.dst_start,
-                             torch.tensor(vals, dtype=torch.float32).reshape(-1, 1, 1))
+                             torch.tensor(vals, dtype=torch.float32).reshape(-1, 1, 1)
+                             .expand(-1, 1, 2).contiguous())
             self.saves.append((rid, sv.dst_start, sv.dst_start + sv.n))
 
     def generate(self, ids, session, max_tokens, load=None, save=False):
