@@ -7,6 +7,8 @@ Each case draws:
   in one to three groups;
 * a destination side: a paged NHD or HND cache through a slot mapping or a block table,
   or flat session stores, in one or two groups;
+* for each side, fused rows (K then V) or split K and V planes, either as strided views
+  of one tensor that holds both planes (``[blocks, 2, ...]``) or as two tensors;
 * one to six spans of up to 240 tokens, with disjoint destinations and deltas of both
   signs, zero and large (the largest cases pass the direct path's four-layer threshold).
 Every destination byte of every layer must equal the oracle's, and no error flag may be
@@ -48,13 +50,57 @@ def _case(seed: int):
     dst_mode = "flat" if dst_layout == "flat" else str(rng.choice(["slots", "table"]))
     src_groups = int(rng.integers(1, 4))
     dst_groups = int(rng.integers(1, 3)) if dst_mode != "slots" else 1
+    # the K/V split of each side from a generator of its own, so that the other draws
+    # stay those of the cases before the split was drawn: 0 fused, 1 planes in one
+    # tensor, 2 planes in two tensors
+    split_rng = np.random.default_rng(10**6 + seed)
+    src_split, dst_split = (int(x) for x in split_rng.integers(0, 3, 2))
     return dict(seed=seed, dtype=dtype, d=d, rotary=rotary, heads=heads, layers=layers,
                 bs=bs, src_layout=src_layout, dst_layout=dst_layout, dst_mode=dst_mode,
-                src_groups=src_groups, dst_groups=dst_groups, rng=rng)
+                src_groups=src_groups, dst_groups=dst_groups, src_split=src_split,
+                dst_split=dst_split, rng=rng)
 
 
 def _paged_shape(blocks, layout, bs, heads, d):
     return (blocks, heads, bs, 2 * d) if layout == "hnd" else (blocks, bs, heads, 2 * d)
+
+
+def _cache_set(caches, layout, bs, split, gpu) -> CacheSet:
+    """A CacheSet on ``gpu`` holding the fused-row CPU tensors ``caches[group][layer]``:
+    as they are (split 0), or as K and V planes -- strided views of one tensor with the
+    two planes on axis 1 (split 1), or two tensors (split 2)."""
+    bs = 1 if layout == "flat" else bs
+    rows = [[t.to(gpu) for t in row] for row in caches]
+    if split == 0:
+        return CacheSet(rows, layout, bs)
+    k_rows, v_rows = [], []
+    for row in rows:
+        ks, vs = [], []
+        for t in row:
+            d = t.shape[-1] // 2
+            if split == 1:
+                both = torch.stack((t[..., :d], t[..., d:]), dim=1).contiguous()
+                ks.append(both[:, 0])
+                vs.append(both[:, 1])
+            else:
+                ks.append(t[..., :d].contiguous())
+                vs.append(t[..., d:].contiguous())
+        k_rows.append(ks)
+        v_rows.append(vs)
+    return CacheSet(k_rows, layout, bs, v_caches=v_rows)
+
+
+def _restore(cs: CacheSet, start) -> None:
+    """Set every (group, layer) cache back to the fused rows ``start[group][layer]``."""
+    for g in range(cs.groups):
+        for layer in range(cs.layers):
+            t0 = start[g][layer]
+            if cs.split:
+                d = t0.shape[-1] // 2
+                cs.caches[g][layer].copy_(t0[..., :d])
+                cs.v_caches[g][layer].copy_(t0[..., d:])
+            else:
+                cs.caches[g][layer].copy_(t0)
 
 
 def _build(c, gpu):
@@ -132,10 +178,8 @@ def _build(c, gpu):
                else None)
     inv = inv_freq(c["rotary"]) if c["rotary"] else None
 
-    src_cs = CacheSet([[t.to(gpu) for t in row] for row in src_caches], c["src_layout"],
-                      1 if c["src_layout"] == "flat" else bs)
-    dst_cs = CacheSet([[t.to(gpu) for t in row] for row in dst_caches], c["dst_layout"],
-                      1 if c["dst_layout"] == "flat" else bs)
+    src_cs = _cache_set(src_caches, c["src_layout"], bs, c["src_split"], gpu)
+    dst_cs = _cache_set(dst_caches, c["dst_layout"], bs, c["dst_split"], gpu)
     plans = [ShiftPlan(spans, src_cs, dst_cs, inv_freq=inv,
                        src_mode="flat" if c["src_layout"] == "flat" else "table",
                        src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
@@ -159,18 +203,17 @@ def test_random_batched_shift_matches_oracle(gpu, seed):
     inv_np = np.zeros(0, np.float32) if inv is None else inv.numpy()
     orc.shift_spans(oracle_spans(spans), src_o, dst_o, inv_np, dname(c["dtype"]),
                     None if k_scale is None else k_scale.numpy())
-    start = [[t.clone() for t in row] for row in dst_cs.caches]
+    start = [[dst_cs.fused(g, layer).clone() for layer in range(dst_cs.layers)]
+             for g in range(dst_cs.groups)]
     for plan in plans:
-        for row, row0 in zip(dst_cs.caches, start):
-            for t, t0 in zip(row, row0):
-                t.copy_(t0)
+        _restore(dst_cs, start)
         flags = torch.zeros(1, dtype=torch.int32, device=gpu)
         plan.launch(error_flags=flags)
         torch.cuda.synchronize(gpu)
         assert int(flags.item()) == 0, plan.direct
-        for g, row in enumerate(dst_cs.caches):
-            for layer, t in enumerate(row):
-                assert np.array_equal(bits(t), dst_o.caches[g][layer]), (
+        for g in range(dst_cs.groups):
+            for layer in range(dst_cs.layers):
+                assert np.array_equal(bits(dst_cs.fused(g, layer)), dst_o.caches[g][layer]), (
                     f"group {g} layer {layer} direct={plan.direct} order={plan.order}")
 
 
