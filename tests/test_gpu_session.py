@@ -458,6 +458,47 @@ def test_block_store_saver_and_loader_match_torch(gpu, store_bs):
                          <= 2.0**-8 * (ref.abs() + 2 * pair) + 1e-6).all())
 
 
+def test_block_store_fp8_saves_and_loads_match_oracle(gpu):
+    """fp8 through the block store, whose fp8 pools keep rows of K then V per head:
+    saves read back bit for bit, and a rotated load out of the pool equals the oracle's
+    fp8 rule with each layer's K scale (V raw)."""
+    import numpy as np
+
+    from oracle import kvshift_oracle as orc
+
+    print("case block store fp8 saves and loads", flush=True)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(17)
+    scales = {f"l{i}": s for i, s in enumerate((0.031, 0.058, 0.092))}
+    kv = {name: (torch.randn(64, H, BS, 2 * D, device=gpu, generator=g) / s)
+          .clamp(-448, 448).to(torch.float8_e4m3fn) for name, s in scales.items()}
+    store = BlockShiftStore(budget_tokens=4096, device=str(gpu), block_size=BS)
+    perm = torch.randperm(64).tolist()
+    sa = Save.from_blocks("a", perm[:30], 3, 3 + 400)
+    assert ShiftSaver(store, BS).save_all(kv, [sa]) == 400 * 3
+    torch.cuda.synchronize(gpu)
+    assert store.pool("l0").shape == (store.pool_blocks, BS, H, 2 * D)  # rows, not planes
+    for name, cache in kv.items():
+        s = slots(perm[:30], 3, 403, BS).to(gpu)
+        want = cache.permute(0, 2, 1, 3)[s // BS, s % BS]
+        got = store.read("a", name, 3, 400)
+        assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), name
+    out = {name: torch.zeros_like(c) for name, c in kv.items()}
+    loader = ShiftLoader(store, BS, inv_freq_for(D, 1e6), k_scales=scales)
+    loader.register_kv_caches(out)
+    dst_blocks = torch.randperm(64).tolist()
+    assert loader.start_load_kv([Load.from_blocks("a", dst_blocks, 60, 60 + 330, 51)]) == 330 * 3
+    torch.cuda.synchronize(gpu)
+    inv = inv_freq_for(D, 1e6).numpy()
+    for name, cache in out.items():
+        s = slots(dst_blocks, 60, 390, BS).to(gpu)
+        got = cache[s // BS, :, s % BS].cpu().view(torch.uint8).numpy()
+        src = store.read("a", name, 9, 330).cpu().view(torch.uint8).numpy()
+        want_k = orc.rotate_k_bits(src[..., :D], 51, inv, "fp8", scales[name])
+        assert np.array_equal(got[..., :D], want_k), name
+        assert np.array_equal(got[..., D:], src[..., D:]), name
+
+
 def test_deferred_per_layer_saves_equal_one_save_all(gpu):
     """vLLM's per-layer hook, deferred: save_kv_layer records, wait_for_save launches
     once; the store ends with the same bytes and the same counters as save_all."""
