@@ -1120,7 +1120,8 @@ def main() -> int:
         "data": "synthetic: K/V ~ N(0,1) bf16 drawn on device (seed 3), shuffled block tables",
         "config": {
             "workload": "qwen3-14b multi-span shift: 40 layers, 8 kv heads, head_dim 128, "
-            "30,720-token history, 8 spans (seed 3), session store blocks (K and V planes, shuffled table) -> HND paged cache (slots)",
+            "30,720-token history, 8 spans (seed 3), session store blocks (K and V "
+            "planes, shuffled table) -> HND paged cache (slots)",
             "tokens_shifted": tokens,
             "layers": 40,
             "spans": 8,
