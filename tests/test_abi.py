@@ -263,3 +263,27 @@ def test_cacheset_takes_a_flat_list_of_layers():
         CacheSet([], "flat")
     with pytest.raises(ValueError, match="empty"):
         CacheSet([[]], "flat")
+
+
+def test_store_planes_and_fused_rows_hold_the_same_rows():
+    """The workloads' session-store blocks in either layout: a K plane then a V plane per
+    block (strided views of one tensor, split K/V caches to the kernels) or rows of K then
+    V; ``CacheSet.fused`` gives the same [..., 2D] rows back from either."""
+    from marathon_amd import workloads as W
+
+    gen = torch.Generator().manual_seed(3)
+    planes = W.store_blocks(5, 4, torch.bfloat16, gen, "cpu", layout="planes")
+    assert planes.shape == (5, 2, 16, 4, 128)
+    cs = W.store_cache_set([[planes]], "planes")
+    assert cs.split and cs.layout == "nhd" and cs.head_size == 128 and cs.heads == 4
+    k, v = cs.caches[0][0], cs.v_caches[0][0]
+    assert k.data_ptr() == planes.data_ptr()
+    assert v.data_ptr() - k.data_ptr() == 16 * 4 * 128 * 2  # the V plane follows the K plane
+    rows = torch.cat((planes[:, 0], planes[:, 1]), dim=-1)  # [5, 16, 4, 256]
+    fused = W.store_cache_set([[rows.contiguous()]], "fused")
+    assert not fused.split and fused.head_size == 128
+    blk, off = torch.tensor([4, 0, 2]), torch.tensor([15, 3, 8])
+    assert torch.equal(cs.fused(0, 0, (blk, off)), fused.fused(0, 0, (blk, off)))
+    assert torch.equal(cs.fused(0, 0), rows)
+    with pytest.raises(ValueError, match="store layout"):
+        W.store_blocks(5, 4, torch.bfloat16, gen, "cpu", layout="hnd")
