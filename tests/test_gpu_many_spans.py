@@ -1,0 +1,91 @@
+"""Span-count limits on the GPU, against the oracle byte for byte.
+
+* More spans than one descriptor takes (``MKV_MAX_SPANS``, 4,096): ``ShiftPlan`` splits
+  them into several plan + shift launches on one workspace, in stream order.
+* The direct path's limit (``MKV_DIRECT_MAX_SPANS``, 63 spans) and one span past it,
+  where ``ShiftPlan`` must fall back to the two-launch path.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from marathon_amd import _lib
+from marathon_amd import workloads as W
+from marathon_amd.spans import CacheSet, ShiftPlan, span_array
+from oracle import kvshift_oracle as orc
+from tests.helpers import bits, inv_freq, oracle_side, oracle_spans
+
+pytestmark = pytest.mark.gpu
+
+HEADS, D, BS, LAYERS = 8, 128, 16, 2
+
+
+def _many_spans(gpu, n_spans: int, seed: int, max_len: int):
+    """n_spans short spans (1..max_len tokens, deltas of both signs and 0) from a store
+    of K/V-plane blocks through a shuffled table into an HND cache through slots, with
+    disjoint destinations."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, max_len + 1, n_spans)
+    total = int(lens.sum())
+    src_hist = total + 64
+    src_blocks = -(-src_hist // BS)
+    dst_hist = total + n_spans * 3 + 64
+    dst_blocks = -(-dst_hist // BS) + 4
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(seed)
+    src = W.store_cache_set([[W.store_blocks(src_blocks, HEADS, torch.bfloat16, gen, gpu)
+                              for _ in range(LAYERS)]])
+    dst = CacheSet([[torch.randn(dst_blocks, HEADS, BS, 2 * D, device=gpu, generator=gen)
+                     .to(torch.bfloat16) for _ in range(LAYERS)]], "hnd", BS)
+    src_table = rng.permutation(src_blocks).astype(np.int32)
+    dst_table = rng.permutation(dst_blocks).astype(np.int64)
+    rows, slots_parts, d_pos, d_off = [], [], 0, 0
+    for n in lens.tolist():
+        s_pos = int(rng.integers(0, src_hist - n + 1))
+        d_pos += int(rng.integers(0, 4))
+        delta = int(rng.choice([0, int(rng.integers(-3000, 3001))]))
+        pos = np.arange(d_pos, d_pos + n)
+        slots_parts.append(dst_table[pos // BS] * BS + pos % BS)
+        rows.append((s_pos, 0, 0, d_off, n, delta, 0, 0))
+        d_pos += n
+        d_off += n
+    spans = span_array(rows)
+    src_index = torch.from_numpy(src_table)
+    dst_index = torch.from_numpy(np.concatenate(slots_parts))
+    return spans, src, dst, src_index, dst_index
+
+
+def _check(gpu, spans, src, dst, src_index, dst_index, **plan_kw):
+    src_o = oracle_side(src, "table", src_index)
+    dst_o = oracle_side(dst, "slots", dst_index)
+    orc.shift_spans(oracle_spans(spans), src_o, dst_o, inv_freq().numpy(), "bf16")
+    plan = ShiftPlan(spans, src, dst, inv_freq=inv_freq(), src_mode="table",
+                     src_index=src_index, dst_mode="slots", dst_index=dst_index, **plan_kw)
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    plan.launch(error_flags=flags)
+    torch.cuda.synchronize(gpu)
+    assert int(flags.item()) == 0
+    for layer in range(LAYERS):
+        got = bits(dst.caches[0][layer])
+        bad = int((got != dst_o.caches[0][layer]).sum())
+        assert bad == 0, f"layer {layer}: {bad} elements differ"
+    return plan
+
+
+@pytest.mark.parametrize("order", ["none", "dst_page"])
+def test_more_spans_than_one_descriptor_takes(gpu, order):
+    n = _lib.MKV_MAX_SPANS + 905
+    print(f"case {n} spans in one plan (several launches), order={order}", flush=True)
+    plan = _check(gpu, *_many_spans(gpu, n, seed=11, max_len=6), direct=False, order=order)
+    assert len(plan.descs) == 2 and not plan.direct
+
+
+@pytest.mark.parametrize("n_spans,direct", [(_lib.MKV_DIRECT_MAX_SPANS, True),
+                                            (_lib.MKV_DIRECT_MAX_SPANS + 1, False)])
+def test_direct_path_span_limit(gpu, n_spans, direct):
+    print(f"case {n_spans} spans, direct path asked for", flush=True)
+    plan = _check(gpu, *_many_spans(gpu, n_spans, seed=12 + n_spans, max_len=9), direct=True)
+    assert plan.direct is direct
