@@ -4,6 +4,8 @@
   them into several plan + shift launches on one workspace, in stream order.
 * The direct path's limit (``MKV_DIRECT_MAX_SPANS``, 63 spans) and one span past it,
   where ``ShiftPlan`` must fall back to the two-launch path.
+* Empty spans among the others (their prefix entries repeat), and a shift with no
+  tokens at all.
 """
 
 from __future__ import annotations
@@ -23,12 +25,14 @@ pytestmark = pytest.mark.gpu
 HEADS, D, BS, LAYERS = 8, 128, 16, 2
 
 
-def _many_spans(gpu, n_spans: int, seed: int, max_len: int):
+def _many_spans(gpu, n_spans: int, seed: int, max_len: int, empty_every: int = 0):
     """n_spans short spans (1..max_len tokens, deltas of both signs and 0) from a store
     of K/V-plane blocks through a shuffled table into an HND cache through slots, with
-    disjoint destinations."""
+    disjoint destinations; every ``empty_every``-th span has no tokens."""
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, max_len + 1, n_spans)
+    if empty_every:
+        lens[::empty_every] = 0
     total = int(lens.sum())
     src_hist = total + 64
     src_blocks = -(-src_hist // BS)
@@ -89,3 +93,29 @@ def test_direct_path_span_limit(gpu, n_spans, direct):
     print(f"case {n_spans} spans, direct path asked for", flush=True)
     plan = _check(gpu, *_many_spans(gpu, n_spans, seed=12 + n_spans, max_len=9), direct=True)
     assert plan.direct is direct
+
+
+@pytest.mark.parametrize("direct", [False, True])
+def test_empty_spans_among_the_others(gpu, direct):
+    print(f"case 40 spans, every third empty, direct={direct}", flush=True)
+    plan = _check(gpu, *_many_spans(gpu, 40, seed=21, max_len=30, empty_every=3),
+                  direct=direct)
+    assert plan.direct is direct
+
+
+def test_a_shift_with_no_tokens_changes_nothing(gpu):
+    print("case spans with no tokens only, and no spans", flush=True)
+    spans, src, dst, src_index, dst_index = _many_spans(gpu, 5, seed=22, max_len=4,
+                                                        empty_every=1)
+    before = [t.clone() for t in dst.caches[0]]
+    for rows in (spans, span_array([])):
+        for direct in (False, True):
+            plan = ShiftPlan(rows, src, dst, inv_freq=inv_freq(), src_mode="table",
+                             src_index=src_index, dst_mode="slots",
+                             dst_index=dst_index[:0], direct=direct)
+            flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+            plan.launch(error_flags=flags)
+            torch.cuda.synchronize(gpu)
+            assert int(flags.item()) == 0
+    for t, t0 in zip(dst.caches[0], before):
+        assert torch.equal(t.view(torch.int16), t0.view(torch.int16))
