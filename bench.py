@@ -809,11 +809,12 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
     loaded by ``ShiftLoader.start_load_kv`` with device-side slots (block tables, not
     slot lists) into an HND paged cache.  Times the whole call from Python (store
     checks, span table, one pinned upload, plan + shift kernels) to the stream's
-    completion, next to the kernels alone on the same plan.  Three steps: the Qwen3-14B
+    completion, next to the kernels alone on the same plan.  The steps: the Qwen3-14B
     multi-span workload's eight spans in bf16 and in fp8 e4m3 (per-layer K scales, as
-    vLLM's ``_k_scale``), and one 29,232-token bf16 load, the size of the reference's
-    in-engine measurement (docs/findings.md:664-666: 34.4 ms copy_ms, 6.2 ms of it the
-    kernel)."""
+    vLLM's ``_k_scale``), into a shuffled destination block table (a long-running
+    engine's) and into an ascending one (a fresh engine's); and one 29,232-token bf16
+    load, the size of the reference's in-engine measurement (docs/findings.md:664-666:
+    34.4 ms copy_ms, 6.2 ms of it the kernel)."""
     import numpy as np
     import torch
 
@@ -832,13 +833,18 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
            "paged cache (40 layers), block tables on the device; medians over steps",
            "reference_in_engine_copy_ms_29232_tokens": 34.4,
            "reference_kernel_ms_29232_tokens": 6.2}
-    multi = lambda: [Load.from_blocks("s", table, int(dst), int(dst) + int(n), int(dl))
-                     for dst, n, dl in zip(lay.dst_start, lay.length, lay.delta)]
+    # a long-running engine's block tables are fragmented (shuffled here); a fresh
+    # engine hands a request ascending blocks (the *_contiguous_dst cases)
+    fresh = np.arange(blocks, dtype=np.int32)
+    multi = lambda tab=table: [Load.from_blocks("s", tab, int(dst), int(dst) + int(n), int(dl))
+                               for dst, n, dl in zip(lay.dst_start, lay.length, lay.delta)]
     for dtype, cases in (
         (torch.bfloat16, {"qwen3_14b_8_spans": multi,
+                          "qwen3_14b_8_spans_contiguous_dst": lambda: multi(fresh),
                           "one_load_29232_tokens":
                               lambda: [Load.from_blocks("s", table, 0, 29232, -186)]}),
-        (torch.float8_e4m3fn, {"qwen3_14b_8_spans_fp8": multi}),
+        (torch.float8_e4m3fn, {"qwen3_14b_8_spans_fp8": multi,
+                               "qwen3_14b_8_spans_fp8_contiguous_dst": lambda: multi(fresh)}),
     ):
         gen = torch.Generator(device=dev)
         gen.manual_seed(0)
@@ -874,6 +880,7 @@ def connector_step(dev, steps: int, warmup: int) -> dict:
                 host.append((t1 - t0) * 1e3)
             plan = loader.last_plan
             _, per = time_plan(plan, steps, warmup, torch.cuda.current_stream(dev))
+            time.sleep(0.005)  # an idle gap that separates the cases in a kernel trace
             kms = float(np.mean(per))
             out[case] = {
                 "dtype": "fp8_e4m3" if fp8 else "bf16",
