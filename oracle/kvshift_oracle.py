@@ -206,9 +206,11 @@ def rotate_f32(kf: np.ndarray, emb_cos: np.ndarray, emb_sin: np.ndarray) -> np.n
     kf = np.asarray(kf, np.float32)
     h = kf.shape[-1] // 2
     rot = np.concatenate((-kf[..., h:], kf[..., :h]), axis=-1)
-    a = kf * emb_cos
-    b = rot * emb_sin
-    return a + b
+    # raw-bit inputs hold NaN and Inf on purpose: IEEE results, no warnings
+    with np.errstate(invalid="ignore", over="ignore"):
+        a = kf * emb_cos
+        b = rot * emb_sin
+        return a + b
 
 
 def rerotate_keys(k: np.ndarray, delta: int, inv: np.ndarray, method: str = "cr") -> np.ndarray:
