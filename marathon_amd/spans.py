@@ -96,18 +96,34 @@ class CacheSet:
             self.v_caches = [list(self.v_caches)]
         if len(self.caches) == 0 or len(self.caches[0]) == 0:
             raise ValueError("empty CacheSet")
+        first = self.caches[0][0]
+        want_dim = 3 if self.layout == "flat" else 4
+        # The kernels address every tensor of the set with one set of strides.  A dim
+        # of one element never advances an address, and torch gives such dims any
+        # stride (a one-row slice is "contiguous" with its parent's strides), so
+        # tensors must agree only where a dim has more than one element, and each
+        # stride of the set comes from a tensor where its dim does.
+        strides = list(first.stride())
+        known = [n > 1 for n in first.shape]
+
+        def agree(t) -> bool:
+            for d, (n, s) in enumerate(zip(t.shape, t.stride())):
+                if n > 1:
+                    if known[d] and s != strides[d]:
+                        return False
+                    strides[d], known[d] = s, True
+            return True
+
         if self.v_caches is not None:
             if len(self.v_caches) != len(self.caches) or any(
                     len(kr) != len(vr) for kr, vr in zip(self.caches, self.v_caches)):
                 raise ValueError("v_caches must match caches group by group, layer by layer")
             for kr, vr in zip(self.caches, self.v_caches):
                 for k, v in zip(kr, vr):
-                    if (k.shape != v.shape or k.stride() != v.stride() or k.dtype != v.dtype
-                            or k.device != v.device):
+                    if (k.shape != v.shape or k.dtype != v.dtype or k.device != v.device
+                            or not agree(k) or not agree(v)):
                         raise ValueError("a V tensor differs from its K tensor in shape, "
                                          "strides, dtype or device")
-        first = self.caches[0][0]
-        want_dim = 3 if self.layout == "flat" else 4
         for row in self.caches:
             if len(row) != len(self.caches[0]):
                 raise ValueError("every group needs the same number of layers")
@@ -116,10 +132,11 @@ class CacheSet:
                     raise ValueError(f"{self.layout} cache must be {want_dim}-D, got {tuple(t.shape)}")
                 if t.dtype != first.dtype or t.device != first.device:
                     raise ValueError("caches differ in dtype or device")
-                if t.shape[1:] != first.shape[1:] or t.stride() != first.stride():
+                if t.shape[1:] != first.shape[1:] or not agree(t):
                     raise ValueError("caches differ in trailing shape or strides")
                 if t.stride(-1) != 1:
                     raise ValueError("rows must be contiguous in the last dimension")
+        self._strides = tuple(strides)
         if self.layout == "flat":
             self.block_size = 1
         elif self.layout == "hnd" and first.shape[2] != self.block_size:
@@ -165,7 +182,8 @@ class CacheSet:
 
     @property
     def strides(self) -> tuple[int, int, int]:
-        s = self.first.stride()
+        """Element strides ``(block or row, head, offset in block)`` of every tensor."""
+        s = self._strides
         if self.layout == "flat":
             return s[0], s[1], 0
         return (s[0], s[1], s[2]) if self.layout == "hnd" else (s[0], s[2], s[1])

@@ -265,6 +265,41 @@ def test_cacheset_takes_a_flat_list_of_layers():
         CacheSet([[]], "flat")
 
 
+def test_cacheset_strides_ignore_dims_of_one_element():
+    """A one-row store cut from a wider tensor keeps its parent's strides (torch calls
+    it contiguous): the set accepts it beside a store of many rows, and addresses every
+    tensor with the strides of the dims that have more than one element."""
+    from marathon_amd.spans import CacheSet
+
+    d = 64
+    short = torch.zeros(1, 1, 2 * d)
+    long = torch.zeros(200, 1, 2 * d)
+    ks = [short[..., :d].contiguous(), long[..., :d].contiguous()]
+    vs = [short[..., d:].contiguous(), long[..., d:].contiguous()]
+    assert ks[0].stride() == (128, 128, 1) and ks[1].stride() == (64, 64, 1)
+    # the row stride is the 200-row store's; the head dim has one element everywhere, so
+    # its stride is the first tensor's (it only ever multiplies head 0)
+    cs = CacheSet([[ks[0]], [ks[1]]], "flat", v_caches=[[vs[0]], [vs[1]]])
+    assert cs.strides == (64, 128, 0)
+    cs = CacheSet([[ks[1]], [ks[0]]], "flat", v_caches=[[vs[1]], [vs[0]]])
+    assert cs.strides == (64, 64, 0)
+    # a real dim that differs is still refused
+    wide = torch.zeros(10, 8, 512)[..., :256]  # rows of 256 at a head stride of 512
+    with pytest.raises(ValueError, match="trailing shape or strides"):
+        CacheSet([[torch.zeros(10, 8, 256)], [wide]], "flat")
+    with pytest.raises(ValueError, match="differs from its K tensor"):
+        CacheSet([[torch.zeros(10, 8, 256)]], "flat", v_caches=[[wide]])
+    # and paged: a one-block cache beside a many-block one, block stride from the latter
+    one = torch.zeros(1, 8, 16, 512)[..., :256]
+    many = torch.zeros(6, 8, 16, 256)
+    with pytest.raises(ValueError, match="trailing shape or strides"):
+        CacheSet([[many], [one]], "hnd", 16)  # its head and offset strides are real
+    blk = torch.zeros(2, 8, 16, 256)[::2]  # one block, at a block stride of two blocks
+    assert blk.shape[0] == 1 and blk.stride(0) == 2 * 8 * 16 * 256
+    for groups in ([[blk], [many]], [[many], [blk]]):
+        assert CacheSet(groups, "hnd", 16).strides == (8 * 16 * 256, 16 * 256, 256)
+
+
 def test_store_planes_and_fused_rows_hold_the_same_rows():
     """The workloads' session-store blocks in either layout: a K plane then a V plane per
     block (strided views of one tensor, split K/V caches to the kernels) or rows of K then
