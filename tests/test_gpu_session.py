@@ -28,7 +28,8 @@ FILLER = "deterministic filler that makes a message worth several blocks of toke
 class RealKVEngine:
     """A paged KV cache with block-level prefix caching, driven by the real decisions."""
 
-    def __init__(self, dev, blocks=1024, seed=0, store="flat", device_slots=False):
+    def __init__(self, dev, blocks=1024, seed=0, store="flat", device_slots=False,
+                 budget=None):
         self.dev = dev
         self.device_slots = device_slots
         g = torch.Generator(device=dev)
@@ -39,10 +40,12 @@ class RealKVEngine:
         self.inv64 = self.inv.to(dev, torch.float64)
         self.kv = {f"layer{i}": torch.zeros(blocks, H, BS, 2 * D, dtype=torch.bfloat16, device=dev)
                    for i in range(LAYERS)}
+        self.budget = budget or (1 << 16 if store == "flat" else 1 << 14)
         if store == "flat":
-            self.store = ShiftStore(budget_tokens=1 << 16, device=str(dev), slab=1024)
+            self.store = ShiftStore(budget_tokens=self.budget, device=str(dev), slab=1024)
         else:
-            self.store = BlockShiftStore(budget_tokens=1 << 14, device=str(dev), block_size=BS)
+            self.store = BlockShiftStore(budget_tokens=self.budget, device=str(dev),
+                                         block_size=BS)
         self.loader = ShiftLoader(self.store, BS, self.inv)
         self.loader.register_kv_caches(self.kv)
         self.saver = ShiftSaver(self.store, BS)
@@ -88,6 +91,8 @@ class RealKVEngine:
                 broken = True
                 blocks.append(self.next_block)
                 self.next_block += 1
+        # host-side bound, before any load or save addresses these blocks
+        assert self.next_block <= self.n_blocks, "the test ran out of paged blocks"
         return blocks, hit
 
     def _verify(self, blocks, ids):
@@ -164,9 +169,9 @@ class ScheduledKVEngine(RealKVEngine):
     def __init__(self, dev, store="flat", device_slots=False, **kw):
         super().__init__(dev, store=store, device_slots=device_slots, **kw)
         if store == "flat":
-            mirror = ShiftStore(budget_tokens=1 << 16, allocate=False, slab=1024)
+            mirror = ShiftStore(budget_tokens=self.budget, allocate=False, slab=1024)
         else:
-            mirror = BlockShiftStore(budget_tokens=1 << 14, allocate=False, block_size=BS)
+            mirror = BlockShiftStore(budget_tokens=self.budget, allocate=False, block_size=BS)
         self.sched = ShiftScheduler(mirror, BS, device_slots=device_slots)
         self.n_req = 0
 
@@ -245,8 +250,7 @@ class ConnectorKVEngine(RealKVEngine):
         super().__init__(dev, store=store, device_slots=True, **kw)
         self.F = F
         extra = {"store_layout": "block" if store == "blocks" else "flat",
-                 "store_tokens": 1 << 14 if store == "blocks" else 1 << 16,
-                 "store_device": str(dev)}
+                 "store_tokens": self.budget, "store_device": str(dev)}
         cfg = F.vllm_config(block_size=BS, extra=extra)
         self.sched = MarathonShiftConnector(cfg, "scheduler")
         self.worker = MarathonShiftConnector(cfg, "worker")
@@ -576,15 +580,36 @@ def test_split_planes_through_the_connector(gpu, store, plane_axis):
     assert all(e["v_exact"] and e["max_rel"] < 4e-3 for e in ls.verify_log)
 
 
-@pytest.mark.parametrize("store,device_slots", [("flat", False), ("blocks", True)])
-def test_random_edit_sessions_through_the_real_kernels(gpu, store, device_slots):
+# more seeds for a longer sweep: MKV_SESSION_CASES=40 python -m pytest tests/test_gpu_session.py
+_SESSION_SEEDS = [5] + list(range(100, 100 + int(__import__("os").environ.get(
+    "MKV_SESSION_CASES", "0"))))
+
+
+@pytest.mark.parametrize("seed", _SESSION_SEEDS)
+@pytest.mark.parametrize("budget", [None, 1200])
+@pytest.mark.parametrize("store,device_slots,engine", [
+    ("flat", False, ScheduledKVEngine), ("blocks", True, ScheduledKVEngine),
+    ("blocks", True, ConnectorKVEngine)])
+def test_random_edit_sessions_through_the_real_kernels(gpu, store, device_slots, engine,
+                                                        budget, seed):
     """Edits anywhere in the history, in three interleaved sessions, every decision
-    through the scheduler half, every load and save through the HIP kernels: after every
-    request every position of every layer holds its token's KV (V bit-exact, K within
-    its shifts' rounding)."""
+    through the scheduler half (or the connector object's hooks), every load and save
+    through the HIP kernels: after every request every position of every layer holds its
+    token's KV (V bit-exact, K within its shifts' rounding).  With a 1,200-token store
+    the sessions evict one another: freed blocks go to other sessions with stale bytes
+    in them, a load the store no longer holds is declined and recomputed, and every
+    position must still hold its own token."""
     from tests.test_scheduler import _random_edit_sessions
 
-    print(f"case random edit sessions store={store} device_slots={device_slots}", flush=True)
-    eng = ScheduledKVEngine(gpu, store=store, device_slots=device_slots)
-    edits = _random_edit_sessions(eng, 5, 14, 3)
-    assert eng.loads == edits > 0, (eng.loads, edits, eng.declines)
+    print(f"case random edit sessions store={store} device_slots={device_slots} "
+          f"engine={engine.__name__} budget={budget} seed={seed}", flush=True)
+    eng = engine(gpu, store=store, device_slots=device_slots, budget=budget)
+    edits = _random_edit_sessions(eng, seed, 14, 3)
+    assert all("store no longer holds" in why or "local hit" in why
+               for why in eng.declines), eng.declines[:3]
+    if budget is None:  # room for every session: every edit turn reuses
+        assert eng.loads == edits, (eng.loads, edits, eng.declines)
+    else:
+        assert eng.loads <= edits, (eng.loads, edits)
+    if seed == _SESSION_SEEDS[0]:  # the default case edits (a sweep's seed may not)
+        assert edits > 0
