@@ -287,7 +287,9 @@ def paged_planes(kv: torch.Tensor, block_size: int):
     ``v`` is None.  5-D: split K and V planes along the axis of size 2, as vLLM's
     ``[2, blocks, bs, heads, D]`` and ``[blocks, 2, bs, heads, D]`` caches hold them;
     ``k`` and ``v`` are the two planes (views), rows ``[D]``.  The layout of the 4-D
-    cache or plane follows :func:`detect_hnd`.
+    cache or plane follows :func:`detect_hnd`.  A split cache of exactly two blocks has
+    the same shape and strides in both forms; it is read as ``[2, blocks, ...]``,
+    vLLM's default.
     """
     shape = tuple(kv.shape)
     if len(shape) == 4:
