@@ -351,7 +351,8 @@ def reference_loop(dev, iters: int = 5) -> dict:
     scattered slot mapping, delta 186.  Host wall clock around the 40 calls
     (synchronised on both sides), best of ``iters`` passes after a warm-up; bytes are
     the source read once plus the destination written once.  One row per token count
-    of its published table (docs/findings.md:644-646, RTX 5090)."""
+    of its published table (docs/findings.md:644-646, RTX 5090).  Beside each, the same
+    loop of 40 launches of torch's elementwise kernel over the same bytes."""
     import numpy as np
     import torch
 
@@ -402,15 +403,35 @@ def reference_loop(dev, iters: int = 5) -> dict:
                 and np.array_equal(gb[:, d:], sb[:, d:])):
             raise AssertionError(f"reference loop output differs from the oracle at n={n}")
         moved = 2 * sum(s.numel() * s.element_size() for s in src)
+        # the same 40-launch loop through torch's elementwise kernel, the same bytes
+        # (each layer's rows read once, written once into a tensor of their size): the
+        # floor that one launch per layer sets on this GPU
+        outs = [torch.empty_like(s) for s in src]
+
+        def torch_loop():
+            for s, o in zip(src, outs):
+                torch.neg(s, out=o)
+
+        warm_up(torch_loop)
+        best_torch = float("inf")
+        for i in range(iters + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            torch_loop()
+            torch.cuda.synchronize()
+            if i:
+                best_torch = min(best_torch, (time.perf_counter() - t0) * 1e3)
         out[f"tokens_{n}"] = {
             "ms": round(best, 4),
             "GB_s": round(moved / (best / 1e3) / 1e9, 1),
             "GiB_s": round(moved / (best / 1e3) / 2**30, 1),
             "us_per_token": round(best * 1e3 / n, 4),
             "host_enqueue_ms": round(host, 4),
+            "torch_neg_loop_ms": round(best_torch, 4),
+            "torch_neg_loop_GB_s": round(moved / (best_torch / 1e3) / 1e9, 1),
             "reference_rtx5090_ms": ref_ms,
         }
-        del src, kv, slots, table
+        del src, kv, slots, table, outs
         torch.cuda.empty_cache()
     return out
 

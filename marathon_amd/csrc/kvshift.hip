@@ -901,13 +901,8 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   for (int lb = 0; lb < LB; ++lb) scale[lb] = 1.0f;
   int cur_span = -1;
   if constexpr (!BATCHED) {
-    if (p.rotate && rot_lane) {
-#pragma unroll
-      for (int e = 0; e < C; ++e) {
-        cs[e] = p.cos[j * C + e];
-        sg[e] = p.sgn[j * C + e];
-      }
-    }
+    // the span's cos/sin are loaded with the first pass's data (phase B), not here: a
+    // load in flight at the pass loop's head would hold back the first data loads
     if constexpr (DT == MKV_FP8_E4M3) {
       if (p.rotate) scale[0] = ld_const(p.k_scale);
     }
@@ -969,6 +964,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     bool live[U];
     int span_u[U], delta_u[U], head_u[U];
     int64_t s_at[U], d_at[U];  // byte offsets of the pass's (first) row
+    int64_t slot_u[U];         // single span: the pass's destination slot, resolved late
     int sb_u[U], db_u[U];      // the (group, layer 0) rows of the base tables
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1055,20 +1051,10 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         delta_u[u] = p.rotate;
         s_at[u] = g * p.src_tstride;
         sb_u[u] = db_u[u] = 0;
-        const int64_t slot = UNIFORM ? ld_const(p.slots + g) : p.slots[g];
-        if (live[u] && (slot < 0 || slot >= p.dst.num_slots)) {
-          if (p.err != nullptr && (!UNIFORM || lane == 0)) atomicOr(p.err, MKV_FLAG_DST_RANGE);
-          live[u] = false;
-        }
-        int64_t blk, off;
-        if (p.dst.bs_shift >= 0) {
-          blk = slot >> p.dst.bs_shift;
-          off = slot & (p.dst.block_size - 1);
-        } else {
-          blk = slot / p.dst.block_size;
-          off = slot - blk * p.dst.block_size;
-        }
-        d_at[u] = blk * p.dst.bstride + off * p.dst.ostride;
+        // the destination slot is only read here; it is checked and turned into an
+        // address after the data loads have gone out (the source row does not need it)
+        slot_u[u] = UNIFORM ? ld_const(p.slots + g) : p.slots[g];
+        d_at[u] = 0;
       }
       if constexpr (BATCHED) live[u] = live[u] && span_u[u] >= 0;
       s_at[u] += head_u[u] * p.src_hstride;
@@ -1152,6 +1138,17 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         }
       }
     }
+    if constexpr (!BATCHED) {
+      // single span: the one rotation table, once per workgroup, behind the data
+      if (cur_span < 0 && p.rotate && rot_lane) {
+#pragma unroll
+        for (int e = 0; e < C; ++e) {
+          cs[e] = p.cos[j * C + e];
+          sg[e] = p.sgn[j * C + e];
+        }
+      }
+      cur_span = 0;
+    }
 #if MKV_TABLE_WITH_DATA
     if constexpr (BATCHED && UNIFORM && DT == MKV_FP8_E4M3) {
       // fp8 (5 waves per SIMD: too few to hide one more dependent round trip per
@@ -1173,18 +1170,45 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
 #endif
     __builtin_amdgcn_sched_barrier(0);
 
+    // xs: the units that store.  A single span's destination slots, read in phase A,
+    // are checked and turned into addresses only now, while the data loads are in
+    // flight: an out-of-range slot raises its flag and its row is not stored.
+    bool xs[N];
+    if constexpr (!BATCHED) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t slot = slot_u[u];
+        const bool ok = slot >= 0 && slot < p.dst.num_slots;
+        if (live[u] && !ok && p.err != nullptr && (!UNIFORM || lane == 0))
+          atomicOr(p.err, MKV_FLAG_DST_RANGE);
+        int64_t blk, off;
+        if (p.dst.bs_shift >= 0) {
+          blk = slot >> p.dst.bs_shift;
+          off = slot & (p.dst.block_size - 1);
+        } else {
+          blk = slot / p.dst.block_size;
+          off = slot - blk * p.dst.block_size;
+        }
+        d_at[u] += blk * p.dst.bstride + off * p.dst.ostride;
+#pragma unroll
+        for (int lb = 0; lb < LB; ++lb) xs[u * LB + lb] = xl[u * LB + lb] && ok;
+      }
+    }
+    // batched shifts resolved their rows in phase A: xl already says what stores
+#define MKV_STORES(x) (BATCHED ? xl[x] : xs[x])
+
     // ---- phase C: V goes out as it came in, then K is rotated (the whole wave joins
     // the partner exchange)
 #if MKV_V_FIRST
 #pragma unroll
     for (int x = 0; x < N; ++x) {
-      if (xl[x] && lane_live) store16(dbv[x] + d_at[x / LB] + d_lane, vd[x]);
+      if (MKV_STORES(x) && lane_live) store16(dbv[x] + d_at[x / LB] + d_lane, vd[x]);
     }
 #endif
 #pragma unroll
     for (int x = 0; x < N; ++x) {
       const int u = x / LB, lb = x % LB;
-      const bool wave_rotates = UNIFORM ? (xl[x] && delta_u[u] != 0 && p.rotary > 0)
+      const bool wave_rotates = UNIFORM ? (MKV_STORES(x) && delta_u[u] != 0 && p.rotary > 0)
                                         : (p.rotary > 0);
       if (!wave_rotates) continue;
       u32x4 pd;
@@ -1192,7 +1216,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
       pd[1] = bpermute(partner_addr, kd[x][1]);
       pd[2] = bpermute(partner_addr, kd[x][2]);
       pd[3] = bpermute(partner_addr, kd[x][3]);
-      if (xl[x] && lane_live && rot_lane && delta_u[u] != 0) {
+      if (MKV_STORES(x) && lane_live && rot_lane && delta_u[u] != 0) {
         if constexpr (BATCHED) {
           if (span_u[u] != cur_span) {
             if constexpr (SMALL) {
@@ -1217,7 +1241,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
 #pragma unroll
     for (int x = 0; x < N; ++x) {
       const int u = x / LB;
-      if (xl[x] && lane_live) {
+      if (MKV_STORES(x) && lane_live) {
         if constexpr (UNIFORM) {
           store16_at(dbk[x] + d_at[u], d_lane, kd[x]);
 #if !MKV_V_FIRST
@@ -1231,6 +1255,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         }
       }
     }
+#undef MKV_STORES
   }
 }
 
