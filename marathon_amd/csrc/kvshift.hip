@@ -965,6 +965,10 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     int span_u[U], delta_u[U], head_u[U];
     int64_t s_at[U], d_at[U];  // byte offsets of the pass's (first) row
     int64_t slot_u[U];         // single span: the pass's destination slot, resolved late
+    // direct: the destination's inputs, resolved late (dchk: span and groups are valid)
+    bool dchk_u[U];
+    int64_t dpos_u[U], didx_u[U], di_u[U];
+    int dg_u[U];
     int sb_u[U], db_u[U];      // the (group, layer 0) rows of the base tables
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1014,19 +1018,19 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         const bool in_span = live[u] && s >= 0 && s < p.n_spans && i >= 0;
         bool ok = in_span && i < n_tok && sg >= 0 && sg < p.src.groups &&
                   dg >= 0 && dg < p.dst.groups;
-        int64_t so = 0, dof = 0;
+        // the source row now; the destination row after the data loads have gone out
+        // (they do not need it), with its inputs kept here
+        dchk_u[u] = ok;
+        dpos_u[u] = dpos;
+        didx_u[u] = didx;
+        di_u[u] = i;
+        dg_u[u] = dg;
+        int64_t so = 0;
         if (ok) {
           const int64_t s_cap = p.src.group_slots != nullptr ? ld_const(p.src.group_slots + sg)
                                                              : p.src.num_slots;
-          const int64_t d_cap = p.dst.group_slots != nullptr ? ld_const(p.dst.group_slots + dg)
-                                                             : p.dst.num_slots;
-          const bool s_ok =
-              resolve_direct(p.src, SMALL ? q->src_index : nullptr, s_cap, spos, sidx, i, so);
-          const bool d_ok =
-              resolve_direct(p.dst, SMALL ? q->dst_index : nullptr, d_cap, dpos, didx, i, dof);
-          if (!(s_ok && d_ok)) {
-            if (p.err != nullptr && lane == 0)
-              atomicOr(p.err, (s_ok ? 0 : MKV_FLAG_SRC_RANGE) | (d_ok ? 0 : MKV_FLAG_DST_RANGE));
+          if (!resolve_direct(p.src, SMALL ? q->src_index : nullptr, s_cap, spos, sidx, i, so)) {
+            if (p.err != nullptr && lane == 0) atomicOr(p.err, MKV_FLAG_SRC_RANGE);
             ok = false;
           }
         } else if (in_span && p.err != nullptr && lane == 0) {
@@ -1035,7 +1039,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         span_u[u] = ok ? s : -1;
         delta_u[u] = delta;
         s_at[u] = so;
-        d_at[u] = dof;
+        d_at[u] = 0;
         sb_u[u] = (ok ? sg : 0) * p.layers;
         db_u[u] = (ok ? dg : 0) * p.layers;
       } else if constexpr (BATCHED) {
@@ -1194,8 +1198,28 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         for (int lb = 0; lb < LB; ++lb) xs[u * LB + lb] = xl[u * LB + lb] && ok;
       }
     }
-    // batched shifts resolved their rows in phase A: xl already says what stores
-#define MKV_STORES(x) (BATCHED ? xl[x] : xs[x])
+    if constexpr (DIRECT) {
+      // the direct path's destination rows, likewise: a row whose source or destination
+      // is out of range raises its flag and is not stored
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int64_t dof = 0;
+        bool d_ok = false;
+        if (dchk_u[u]) {
+          const int64_t d_cap = p.dst.group_slots != nullptr
+                                    ? ld_const(p.dst.group_slots + dg_u[u])
+                                    : p.dst.num_slots;
+          d_ok = resolve_direct(p.dst, SMALL ? q->dst_index : nullptr, d_cap, dpos_u[u],
+                                didx_u[u], di_u[u], dof);
+          if (!d_ok && p.err != nullptr && lane == 0) atomicOr(p.err, MKV_FLAG_DST_RANGE);
+        }
+        d_at[u] += dof;
+#pragma unroll
+        for (int lb = 0; lb < LB; ++lb) xs[u * LB + lb] = xl[u * LB + lb] && d_ok;
+      }
+    }
+    // the record path resolved its rows in phase A: xl already says what stores
+#define MKV_STORES(x) ((BATCHED && !DIRECT) ? xl[x] : xs[x])
 
     // ---- phase C: V goes out as it came in, then K is rotated (the whole wave joins
     // the partner exchange)
