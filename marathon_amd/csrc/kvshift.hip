@@ -900,24 +900,12 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
 #pragma unroll
   for (int lb = 0; lb < LB; ++lb) scale[lb] = 1.0f;
   int cur_span = -1;
-  if constexpr (!BATCHED) {
-    // the span's cos/sin are loaded with the first pass's data (phase B), not here: a
-    // load in flight at the pass loop's head would hold back the first data loads
-    if constexpr (DT == MKV_FP8_E4M3) {
-      if (p.rotate) scale[0] = ld_const(p.k_scale);
-    }
-  } else {
-    // the scale dequantises K for the rotation; with rotary 0 nothing is rotated and
-    // k_scale may be NULL
-    if constexpr (DT == MKV_FP8_E4M3) {
-      if (p.rotary > 0) {
+  // a single span's cos/sin and fp8's K scales are loaded behind the first pass's data
+  // (phase B), not here: they are needed only for the rotation, and a load in flight at
+  // the pass loop's head would hold back the first data loads
+  bool scale_ready = DT != MKV_FP8_E4M3;
 #pragma unroll
-        for (int lb = 0; lb < LB; ++lb) scale[lb] = ld_const(p.k_scale + lay[lb]);
-      }
-    }
-  }
-#pragma unroll
-  for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f / scale[lb];  // correctly rounded
+  for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f;
 
   // direct (span table in memory): lane k holds span k's fields and prefix entry k,
   // loaded once; a pass finds its span with one ballot and reads the fields from that
@@ -1140,6 +1128,18 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
           kd[x] = load16(sbk[x] + s_at[u] + s_lane);
           vd[x] = load16(sbv[x] + s_at[u] + s_lane);
         }
+      }
+    }
+    if constexpr (DT == MKV_FP8_E4M3) {
+      if (!scale_ready) {
+        // the scale dequantises K for the rotation; with no rotation k_scale may be NULL
+        if (BATCHED ? p.rotary > 0 : p.rotate != 0) {
+#pragma unroll
+          for (int lb = 0; lb < LB; ++lb) scale[lb] = ld_const(p.k_scale + (BATCHED ? lay[lb] : 0));
+        }
+#pragma unroll
+        for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f / scale[lb];  // correctly rounded
+        scale_ready = true;
       }
     }
     if constexpr (!BATCHED) {
