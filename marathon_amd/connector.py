@@ -746,7 +746,7 @@ class ShiftSaver:
             else:
                 bufs[g] = targets  # a save may have grown (reallocated) the buffers
             taken.append(save)
-        if blocky:
+        if blocky and len(taken) > 1:
             # a later save of the same call may have truncated an earlier one's blocks
             taken = [sv for sv in taken if self.store.holds_blocks(sv.session, sv.dst_start, sv.n)]
         if not taken:
