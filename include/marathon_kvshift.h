@@ -250,8 +250,8 @@ int mkv_shift_spans(const mkv_shift_desc_t* desc, void* stream);
  *   - n_spans <= MKV_SMALL_MAX_SPANS and each side's index_len <= MKV_SMALL_MAX_INDEX;
  *     both sides' block sizes powers of two; heads a multiple of the rows one wave covers
  *     (64 / (head_size * element bytes / 16)); otherwise MKV_ERR_UNSUPPORTED;
- *   - the token prefix is computed here: a span with n_tokens < 0, or spans that hold
- *     more than total_tokens tokens, are MKV_ERR_ARG;
+ *   - the token prefix is computed here: a span with n_tokens < 0, or spans whose
+ *     n_tokens do not sum to total_tokens, are MKV_ERR_ARG;
  *   - the rotation tables are computed in the kernel from inv_freq as the plan pass
  *     computes them; desc->workspace, span_starts and span_tables are ignored.
  * Replaces the reference connector's per-layer, per-save launches for a decode step
@@ -273,6 +273,10 @@ int mkv_shift_spans_small(const mkv_shift_desc_t* desc, void* stream);
  *   - Every call on one GPU shares that GPU's buffer, which keeps the last call's
  *     contents: calls that overlap on one GPU (on different streams, or from different
  *     threads without ordering) race.  Calls ordered on one stream do not.
+ *   - The first call on a GPU resolves that GPU's buffer address (hipGetSymbolAddress);
+ *     make that call eagerly, before capturing calls into a HIP graph.  A captured call
+ *     records its kernels only (no memset or copy nodes), and each replay reuses the
+ *     buffer: graphs of this entry point must not replay concurrently on one GPU.
  */
 int mkv_shift_spans_noalloc(const mkv_shift_desc_t* desc, void* stream);
 #define MKV_NOALLOC_SCRATCH_BYTES (16LL << 20)

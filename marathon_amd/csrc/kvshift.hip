@@ -1828,7 +1828,9 @@ extern "C" int mkv_shift_spans_small(const mkv_shift_desc_t* d, void* stream) {
     acc += d->spans[k].n_tokens;
   }
   for (int k = d->n_spans; k <= MKV_SMALL_MAX_SPANS; ++k) a.q.starts[k] = acc;
-  if (acc > d->total_tokens)
+  // the prefix is computed here, so a total that disagrees with it is the caller's error
+  // (fewer would leave tokens unmoved, more would launch workgroups with no span)
+  if (acc != d->total_tokens)
     return fail(MKV_ERR_ARG, "the spans hold %lld tokens, total_tokens is %lld", (long long)acc,
                 (long long)d->total_tokens);
   rc = pack_index(d->src, a.q.src_index, "src");

@@ -69,15 +69,41 @@ def inv_freq_for(head_dim: int, rope_theta: float, partial_rotary_factor: float 
     return 1.0 / (float(rope_theta) ** (torch.arange(0, rotary, 2, dtype=torch.float32) / rotary))
 
 
-def rope_shift(delta: int, head_size: int, inv_freq: torch.Tensor, device) -> RopeShift:
+def shift_rotary(shift) -> int:
+    """Rotated dimensions of a ``RopeShift``: the length of its ``emb_cos`` table, which
+    ``rope_shift`` builds from the ``rotary / 2`` angles (shift_kernels.py:73, :83-84).
+    Works for this package's ``RopeShift`` and for the reference's, which has no
+    ``rotary`` field; a ``rotary`` field that disagrees with the table is refused."""
+    if shift is None:
+        return 0
+    rotary = int(shift.emb_cos.numel())
+    declared = getattr(shift, "rotary", None)
+    if declared is not None and int(declared) != rotary:
+        raise ValueError(f"RopeShift.rotary {declared} != len(emb_cos) {rotary}")
+    return rotary
+
+
+TABLES = ("exact", "reference")
+
+
+def rope_shift(delta: int, head_size: int, inv_freq: torch.Tensor, device,
+               tables: str = "exact") -> RopeShift:
     """Tables that move RoPE'd keys ``delta`` positions (shift_kernels.py:68-84).
 
-    cos/sin are the exact values of the fp32 angles ``fl32(delta * inv_freq)`` rounded
-    once to fp32 -- the same numbers the kernel computes on the device.
+    ``tables="exact"`` (the default): cos/sin are the exact values of the fp32 angles
+    ``fl32(delta * inv_freq)`` rounded once to fp32 -- the same numbers the kernel
+    computes on the device.  ``tables="reference"``: the reference's own tables, built
+    as its ``rope_shift`` builds them, with torch's fp32 ``cos``/``sin`` on ``device``;
+    through :func:`scatter_shifted` these reproduce the reference's torch path
+    (shift_kernels.py:141-159) bit for bit.
     """
+    if tables not in TABLES:
+        raise ValueError(f"tables must be one of {TABLES}, not {tables!r}")
     rotary = 2 * int(inv_freq.numel())
     assert rotary <= head_size, f"rotary {rotary} > head_size {head_size}"
     half = rotary // 2
+    if tables == "reference":
+        return _reference_tables(delta, head_size, inv_freq, device, rotary)
     inv = inv_freq.detach().to(device="cpu", dtype=torch.float32).numpy()
     ang = (np.float32(delta) * inv).astype(np.float64)
     c = np.cos(ang).astype(np.float32)
@@ -106,6 +132,27 @@ def rope_shift(delta: int, head_size: int, inv_freq: torch.Tensor, device) -> Ro
         dev(inv.copy()),
         rotary,
     )
+
+
+def _reference_tables(delta: int, head_size: int, inv_freq: torch.Tensor, device,
+                      rotary: int) -> RopeShift:
+    """The reference's table construction (shift_kernels.py:72-84), in torch fp32 on
+    ``device``: one fp32 multiply per angle, then torch's fp32 ``cos``/``sin`` of
+    ``cat(ang, ang)``."""
+    half = rotary // 2
+    inv = inv_freq.detach().to(device=device, dtype=torch.float32)
+    ang = float(delta) * inv
+    emb = torch.cat((ang, ang))
+    emb_cos, emb_sin = emb.cos(), emb.sin()
+    cos = torch.ones(head_size, dtype=torch.float32, device=device)
+    sgn = torch.zeros(head_size, dtype=torch.float32, device=device)
+    cos[:rotary] = emb_cos
+    sgn[:half] = -emb_sin[:half]
+    sgn[half:rotary] = emb_sin[half:rotary]
+    partner = torch.arange(head_size, dtype=torch.int32, device=device)
+    partner[:half] += half
+    partner[half:rotary] -= half
+    return RopeShift(int(delta), cos, sgn, partner, emb_cos, emb_sin, inv.contiguous(), rotary)
 
 
 def use_hip(kv: torch.Tensor) -> bool:
@@ -143,13 +190,28 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# fp32 K scales given as Python numbers, kept on their device: the reference's
+# per-layer loop passes the same 40 scales on every load, so each is uploaded once
+_SCALES: dict[tuple[int, int], torch.Tensor] = {}
+_SCALES_MAX = 4096
+
+
 def _scale_tensor(k_scale, device) -> torch.Tensor:
     if isinstance(k_scale, torch.Tensor):
         t = k_scale.detach().reshape(-1)[:1]
         if t.device != device or t.dtype != torch.float32:
             t = t.to(device=device, dtype=torch.float32)
         return t.contiguous()
-    return torch.tensor([float(k_scale)], dtype=torch.float32, device=device)
+    value = np.float32(float(k_scale))
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (int(idx), int(value.view(np.uint32)))  # by bits: -0.0 and NaN stay distinct
+    t = _SCALES.get(key)
+    if t is None:
+        if len(_SCALES) >= _SCALES_MAX:
+            _SCALES.clear()
+        t = torch.tensor([value], dtype=torch.float32, device=torch.device("cuda", idx))
+        _SCALES[key] = t
+    return t
 
 
 def scatter_shifted(
@@ -194,7 +256,11 @@ def scatter_shifted(
         slots = slots.to(device=kv.device, dtype=torch.int64, non_blocking=True).contiguous()
     if slots.numel() != n:
         raise ValueError(f"{slots.numel()} slots for {n} tokens")
-    rotate = shift is not None and shift.delta != 0 and shift.rotary > 0
+    # the rotary width is the length of emb_cos (rope_shift builds it from the rotary/2
+    # angles, shift_kernels.py:73, :83-84): host metadata, so a reference-built RopeShift
+    # (no ``rotary`` field) of a partial-rotary model needs nothing more from the caller
+    rotary = shift_rotary(shift)
+    rotate = shift is not None and shift.delta != 0 and rotary > 0
     cos = sgn = scale = None
     if rotate:
         cos, sgn = shift.cos, shift.sgn
@@ -225,7 +291,7 @@ def scatter_shifted(
         code,
         None if cos is None else cos.data_ptr(),
         None if sgn is None else sgn.data_ptr(),
-        shift.rotary if rotate else 0,
+        rotary if rotate else 0,
         None if scale is None else scale.data_ptr(),
         None if error_flags is None else error_flags.data_ptr(),
         ctypes.c_void_p(int(stream)),

@@ -127,6 +127,11 @@ class CacheSet:
         for row in self.caches:
             if len(row) != len(self.caches[0]):
                 raise ValueError("every group needs the same number of layers")
+            # the device bounds-checks a group's slots against one capacity (its first
+            # layer's), so every layer of a group must hold as many blocks / rows
+            if any(t.dim() > 0 and t.shape[0] != row[0].shape[0] for t in row):
+                raise ValueError("the layers of a group differ in their number of blocks / "
+                                 f"rows: {sorted({int(t.shape[0]) for t in row})}")
             for t in row:
                 if t.dim() != want_dim:
                     raise ValueError(f"{self.layout} cache must be {want_dim}-D, got {tuple(t.shape)}")

@@ -145,6 +145,7 @@ class MarathonShiftConnector(_ConnectorBase):
                                    k_scales=self._k_scales)
         self._saver = ShiftSaver(self._store, self._bs, deferred=True)
         self._registered = False
+        self._scales_read = False
 
     @property
     def store(self):
@@ -215,8 +216,8 @@ class MarathonShiftConnector(_ConnectorBase):
                     len(kv_caches), self._loader.layout, self._store.budget)
 
     def _register_from(self, forward_context) -> None:
-        """The caches (and fp8 K scales) of the attention layers of a forward pass, as
-        the reference takes them when none were registered (:484-493)."""
+        """The caches of the attention layers of a forward pass, as the reference takes
+        them when none were registered (:484-493)."""
         ve = getattr(forward_context, "virtual_engine", 0)
         caches = {}
         for name, layer in forward_context.no_compile_layers.items():
@@ -224,13 +225,21 @@ class MarathonShiftConnector(_ConnectorBase):
             if kv is None:
                 continue
             caches[name] = kv[ve] if isinstance(kv, list) else kv
+        if caches:
+            self.register_kv_caches(caches)
+
+    def _scales_from(self, forward_context) -> None:
+        """The fp8 K scales of the attention layers (``_k_scale_float``, else
+        ``_k_scale``), read once from the first forward pass that loads, whichever way
+        the caches were registered: vLLM's own ``register_kv_caches`` call passes only
+        the tensors.  A layer with no scale keeps 1.0."""
+        for name, layer in forward_context.no_compile_layers.items():
             scale = getattr(layer, "_k_scale_float", None)
             if scale is None and getattr(layer, "_k_scale", None) is not None:
                 scale = float(layer._k_scale)
             if scale is not None:
                 self._k_scales[name] = float(scale)
-        if caches:
-            self.register_kv_caches(caches)
+        self._scales_read = True
 
     def start_load_kv(self, forward_context, **kwargs) -> None:
         """Every load of the step in one launch, before the forward pass
@@ -240,6 +249,8 @@ class MarathonShiftConnector(_ConnectorBase):
             return
         if not self._registered:
             self._register_from(forward_context)
+        if not self._scales_read:
+            self._scales_from(forward_context)
         t0 = 0.0
         if self._timing:
             torch.cuda.synchronize()

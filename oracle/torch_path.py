@@ -35,7 +35,38 @@ def rope_shift_tables(delta: int, head_size: int, inv_freq: torch.Tensor, device
     sgn = torch.zeros(head_size, dtype=torch.float32, device=device)
     sgn[:half] = -sin[:half]
     sgn[half:rotary] = sin[half:rotary]
-    return {"cos": cos, "sgn": sgn, "emb_cos": emb.cos(), "emb_sin": sin}
+    partner = torch.arange(head_size, dtype=torch.int32, device=device)
+    partner[:half] += half
+    partner[half:rotary] -= half
+    return {"cos": cos, "sgn": sgn, "partner": partner, "emb_cos": emb.cos(), "emb_sin": sin}
+
+
+def triton_rows_into_paged(
+    rows: torch.Tensor,
+    cache: torch.Tensor,
+    slot: torch.Tensor,
+    block_size: int,
+    hnd: bool,
+    tables: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None,
+) -> None:
+    """One layer as the reference's Triton kernel computes it (shift_kernels.py:117-132),
+    on the CPU: ``k * cos + k[partner] * sgn`` in fp32 with the ``[head_size]`` tables
+    of ``rope_shift`` (cos, sgn, partner), as separate multiplies and one add, cast back
+    to the cache dtype; V copied.  This is the reference's only path that handles
+    partial rotary: its torch path multiplies the ``[head_size]`` keys by the
+    ``[rotary]`` ``emb_cos`` and cannot broadcast them when rotary < head_size
+    (:153-156).  For finite keys, the dimensions past ``rotary`` come out as
+    ``k * 1 + k * 0 = k``.  ``tables`` of ``None`` is a delta-0 plain scatter."""
+    d = rows.shape[-1] // 2
+    keys = rows[..., :d]
+    if tables is not None:
+        cos, sgn, partner = (t.cpu() for t in tables)
+        kf = keys.to(torch.float32)
+        kp = kf[..., partner.long()]
+        keys = (kf * cos + kp * sgn).to(cache.dtype)
+    block, offset = slot // block_size, slot % block_size
+    where = (block, slice(None), offset) if hnd else (block, offset)
+    cache[where] = torch.cat((keys, rows[..., d:]), dim=-1)
 
 
 def shift_into_paged(

@@ -8,6 +8,7 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 import torch
 
@@ -192,9 +193,10 @@ def test_small_entry_point_checks_its_limits_without_a_gpu():
     d.n_spans, d.total_tokens = 9, 18
     assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_UNSUPPORTED
     d.n_spans = 2
-    d.total_tokens = 3  # the spans hold 4
-    assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
-    assert b"total_tokens" in lib.mkv_last_error()
+    for total in (3, 5):  # the spans hold 4: fewer and more are both refused
+        d.total_tokens = total
+        assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+        assert b"total_tokens" in lib.mkv_last_error()
     spans["n_tokens"][0] = -1
     d.total_tokens = 4
     assert lib.mkv_shift_spans_small(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
@@ -322,3 +324,65 @@ def test_store_planes_and_fused_rows_hold_the_same_rows():
     assert torch.equal(cs.fused(0, 0), rows)
     with pytest.raises(ValueError, match="store layout"):
         W.store_blocks(5, 4, torch.bfloat16, gen, "cpu", layout="hnd")
+
+
+def test_cacheset_refuses_a_group_whose_layers_differ_in_length():
+    """The device checks a group's slots against one capacity, its first layer's: a
+    shorter (or longer) layer in the same group would let a slot past its end through, so
+    the set refuses it.  Groups may still differ from one another."""
+    from marathon_amd.spans import CacheSet
+
+    with pytest.raises(ValueError, match="layers of a group differ"):
+        CacheSet([torch.zeros(8, 8, 16, 256), torch.zeros(6, 8, 16, 256)], "hnd", 16)
+    with pytest.raises(ValueError, match="layers of a group differ"):
+        CacheSet([[torch.zeros(100, 8, 256), torch.zeros(120, 8, 256)]], "flat")
+    cs = CacheSet([[torch.zeros(8, 8, 16, 256)] * 2, [torch.zeros(6, 8, 16, 256)] * 2], "hnd", 16)
+    _, _, caps, low, uniform = cs.base_tables()
+    assert caps.tolist() == [128, 96] and low == 96 and not uniform
+
+
+def test_dropin_and_rotary_width_on_the_host():
+    """The reference-side binding refuses a CPU cache (no CPU path), and both bindings
+    take the rotary width from ``emb_cos`` (host metadata) -- a reference-shaped
+    ``RopeShift`` with no ``rotary`` field works, a contradicting field is refused."""
+    from types import SimpleNamespace
+
+    from marathon_amd.shift_kernels import shift_rotary
+    from marathon_amd.shift_kernels_hip import scatter_shifted as dropin
+
+    inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2, dtype=torch.float32) / 64))
+    shift = rope_shift(7, 128, inv, "cpu")
+    assert shift_rotary(shift) == 64 and shift_rotary(None) == 0
+    ref_shaped = SimpleNamespace(delta=7, cos=shift.cos, sgn=shift.sgn, partner=shift.partner,
+                                 emb_cos=shift.emb_cos, emb_sin=shift.emb_sin)
+    assert shift_rotary(ref_shaped) == 64
+    ref_shaped.rotary = 128
+    with pytest.raises(ValueError, match="rotary"):
+        shift_rotary(ref_shaped)
+    src = torch.zeros(4, 8, 256, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 8, 16, 256, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        dropin(src, kv, torch.arange(4), 16, True, shift)
+
+
+def test_rope_shift_reference_tables_are_the_reference_construction():
+    """``tables="reference"`` builds the reference's tables with torch fp32 (on the CPU
+    here): the same bits as the reference's construction restated in oracle/torch_path.py
+    (shift_kernels.py:68-84); the default tables are the correctly rounded ones."""
+    from oracle import kvshift_oracle as orc
+    from oracle import torch_path
+
+    for rotary in (128, 64):
+        inv = 1.0 / (1e6 ** (torch.arange(0, rotary, 2, dtype=torch.float32) / rotary))
+        for delta in (-3000, 186, 2**25 + 1):
+            got = rope_shift(delta, 128, inv, "cpu", tables="reference")
+            want = torch_path.rope_shift_tables(delta, 128, inv, "cpu")
+            for name in ("cos", "sgn", "partner", "emb_cos", "emb_sin"):
+                assert torch.equal(getattr(got, name), want[name]), name
+            assert got.rotary == rotary
+            exact = rope_shift(delta, 128, inv, "cpu")
+            c, s = orc.cos_sin(delta, inv.numpy())
+            assert np.array_equal(exact.emb_cos.numpy()[: rotary // 2], c)
+            assert np.array_equal(exact.emb_sin.numpy()[: rotary // 2], s)
+    with pytest.raises(ValueError, match="tables"):
+        rope_shift(1, 128, inv, "cpu", tables="torch")

@@ -277,7 +277,7 @@ def test_qwen3_0_6b_shift_through_both_entry_points(gpu):
     plan.launch(error_flags=flags)
     torch.cuda.synchronize(gpu)
     assert int(flags.item()) == 0
-    beyond, worst_abs, src_max = 0, 0.0, 0.0
+    beyond, worst_abs, src_max, worst_ulp = 0, 0.0, 0.0, 0
     for layer in range(layers):
         sb = bits(wl["src"][layer])
         want = bits(wl["kv"][layer])
@@ -291,10 +291,16 @@ def test_qwen3_0_6b_shift_through_both_entry_points(gpu):
         torch_path.shift_into_paged(wl["src"][layer], ref, slots, 16, True,
                                     torch_path.rope_emb_tables(delta, inv))
         got_k, ref_k = want[blk, :, off][..., :D], bits(ref)[blk, :, off][..., :D]
-        beyond += int((ulp_bf16(got_k, ref_k) > 1).sum())
+        ulps = ulp_bf16(got_k, ref_k)
+        beyond += int((ulps > 1).sum())
+        worst_ulp = max(worst_ulp, int(ulps.max()))
         assert bool(within_table_rounding(got_k, ref_k, sb[..., :D], D).all()), layer
         worst_abs = max(worst_abs, float(np.abs(orc.bf16_to_f32(got_k) - orc.bf16_to_f32(ref_k)).max()))
         src_max = max(src_max, float(np.abs(orc.bf16_to_f32(sb)).max()))
     # the reference test's own bounds (tests/test_shift_kernels.py:75-78)
+    total = layers * 4096 * 8 * D
+    print(f"config 1 K vs the torch path with torch's tables: {beyond} of {total} elements "
+          f"more than 1 bf16 ulp apart ({beyond / total:.3e}); max |diff| {worst_abs:.3e}, "
+          f"max ulp {worst_ulp}", flush=True)
     assert worst_abs <= 2**-7 * src_max
-    assert beyond / (layers * 4096 * 8 * D) < 1e-3
+    assert beyond / total < 1e-3

@@ -194,6 +194,35 @@ def test_bf16_rotation_is_the_reference_op_sequence(delta):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("rotary", [128, 64, 32])
+@pytest.mark.parametrize("delta", [-3000, -566, 4, 186, 10000])
+def test_triton_arithmetic_restatement_is_the_rotate_half_rotation(rotary, delta):
+    """``torch_path.triton_rows_into_paged`` (the Triton kernel's ``k*cos + k[partner]*sgn``
+    through the ``[head_size]`` tables) equals the oracle's ``cat``-based rotate-half
+    (kvshift.py:44-46) with the same torch tables, bit for bit, at full and partial
+    rotary; at full rotary it also equals the torch path.  A wrong partner table fails."""
+    g = torch.Generator().manual_seed(rotary + delta % 101)
+    rows = torch.randn(40, 8, 256, generator=g).to(torch.bfloat16)
+    slot = torch.randperm(64, generator=g)[:40]
+    inv = torch.from_numpy(_inv(rotary))
+    t = torch_path.rope_shift_tables(delta, 128, inv, "cpu")
+    kv = torch.zeros(4, 8, 16, 256, dtype=torch.bfloat16)
+    torch_path.triton_rows_into_paged(rows, kv, slot, 16, True, (t["cos"], t["sgn"], t["partner"]))
+    got = kv.view(torch.int16).numpy().view(np.uint16)
+    want = np.zeros_like(got)
+    orc.scatter_shifted(rows.view(torch.int16).numpy().view(np.uint16), want, slot.numpy(), 16,
+                        True, delta, inv.numpy(), "bf16", method="torch")
+    assert np.array_equal(got, want)
+    if rotary == 128:
+        ref = torch.zeros_like(kv)
+        torch_path.shift_into_paged(rows, ref, slot, 16, True, (t["emb_cos"], t["emb_sin"]))
+        assert torch.equal(ref.view(torch.int16), kv.view(torch.int16))
+    wrong = torch.arange(128, dtype=torch.int32)  # identity partner: no rotate-half
+    bad = torch.zeros_like(kv)
+    torch_path.triton_rows_into_paged(rows, bad, slot, 16, True, (t["cos"], t["sgn"], wrong))
+    assert not np.array_equal(bad.view(torch.int16).numpy().view(np.uint16), want)
+
+
 @pytest.mark.parametrize("hnd", [True, False])
 @pytest.mark.parametrize("delta", [0, 1, -1, 17, -17, 566, -566, -1133, 6759])
 def test_scatter_lands_what_rerotate_keys_says_qwen3_geometry(delta, hnd):

@@ -114,3 +114,28 @@ def test_stats_merge_every_store():
     after = vc.stats()  # the module-wide view includes these two stores
     assert after["hits"] - before["hits"] >= 2
     del sched, worker
+
+
+def test_fp8_k_scales_are_read_when_vllm_registered_the_caches(monkeypatch):
+    """vLLM's worker calls ``register_kv_caches`` itself with tensors only; the layers' K
+    scales still come from the first loading forward pass (``_k_scale_float``), so the two
+    registration routes requantise fp8 K with the same scales."""
+    for registered in (True, False):
+        _, worker = _pair()
+        caches = {f"l{i}": torch.zeros(4, 8, 16, 256, dtype=torch.float8_e4m3fn) for i in range(3)}
+        scales = {"l0": 0.05, "l1": 0.0125, "l2": 0.1}
+        if registered:
+            worker.register_kv_caches(caches)
+        seen = {}
+
+        def fake_load(loads, _seen=seen, _w=worker):
+            _seen.update(_w._loader.k_scales)
+            return 0
+
+        monkeypatch.setattr(worker._loader, "register_kv_caches", lambda kv: None)
+        monkeypatch.setattr(worker._loader, "start_load_kv", fake_load)
+        worker.bind_connector_metadata(vc.ShiftConnectorMetadata(
+            loads=[Load.from_blocks("s", [0], 0, 16, 0)]))
+        worker.start_load_kv(F.forward_context(caches, k_scales=scales))
+        assert seen == scales, registered
+        assert worker._loader.k_scales is worker._k_scales

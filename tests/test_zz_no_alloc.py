@@ -95,3 +95,57 @@ def test_noalloc_batched_sessions(gpu):
         _run_case(gpu, wl)
         del wl
         torch.cuda.empty_cache()
+
+
+def test_noalloc_replayed_from_a_captured_graph(gpu):
+    """The no-allocation entry point's own use case: a call captured in a HIP graph
+    (``torch.cuda.graph``) after one eager call on the device has resolved the scratch
+    address, then replayed five times, with the program's own eager work (restoring the
+    destination, clearing the flags with a fill kernel: no memset node is captured) and a
+    synchronisation between replays.  Every replay must write the oracle's bytes."""
+    L = _lib.lib()
+    wl = W.qwen3_14b_multispan(gpu, layers=2, history=2048, dst_fill="random")
+    want = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
+    orc.shift_spans(oracle_spans(wl.spans), oracle_side(wl.src, wl.src_mode, wl.src_index),
+                    want, wl.inv_freq.numpy(), dname(wl.dst.first.dtype))
+    pristine = [c.clone() for c in wl.dst.caches[0]]
+    plan = wl.plan(direct=False)
+    assert not plan.direct
+    torch.cuda.synchronize(gpu)
+    flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+    descs = []
+    for d in plan.descs:
+        nd = _noalloc_desc(d)
+        nd.error_flags = flags.data_ptr()
+        descs.append(nd)
+
+    def check(tag):
+        assert int(flags.item()) == 0, tag
+        for layer in range(wl.layers):
+            got = bits(wl.dst.caches[0][layer])
+            assert np.array_equal(got, want.caches[0][layer]), f"{tag}: layer {layer} differs"
+
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):  # the eager call that resolves the scratch address
+        for nd in descs:
+            _lib.check(L.mkv_shift_spans_noalloc(ctypes.byref(nd),
+                                                 ctypes.c_void_p(side.cuda_stream)))
+    torch.cuda.synchronize(gpu)
+    check("eager")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for nd in descs:
+            _lib.check(L.mkv_shift_spans_noalloc(ctypes.byref(nd),
+                                                 ctypes.c_void_p(side.cuda_stream)))
+    torch.cuda.synchronize(gpu)
+    for replay in range(5):
+        print(f"case no-alloc graph replay {replay}", flush=True)
+        for c, p in zip(wl.dst.caches[0], pristine):
+            c.copy_(p)
+        flags.zero_()
+        torch.cuda.synchronize(gpu)
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        check(f"replay {replay}")
+    del graph
