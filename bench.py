@@ -157,7 +157,53 @@ def host_cores() -> dict:
     return {"os_cpu_count": os.cpu_count(), "usable": usable}
 
 
-def cpu_baseline(reps: int = 5, gpu_small: dict | None = None) -> dict:
+def _loadavg() -> list | None:
+    try:
+        return [round(x, 2) for x in os.getloadavg()]
+    except OSError:
+        return None
+
+
+def _spread(seconds: list) -> dict:
+    """min / median / max of timed passes, in ms."""
+    import numpy as np
+
+    ms = np.array(seconds) * 1e3
+    return {"n": len(seconds), "min": round(float(ms.min()), 2),
+            "median": round(float(np.median(ms)), 2), "max": round(float(ms.max()), 2)}
+
+
+def _k_vs_torch_path(small: dict, gpu_out: dict) -> dict:
+    """K of the Qwen3-0.6B shift written by the HIP path, against the reference's torch
+    path on the CPU (``small["kv"]`` after the timed passes), over every element of the
+    shifted rows of all 28 layers: with this package's correctly rounded tables (count
+    and fraction more than 1 bf16 ulp apart, max ulp), and with the reference's own
+    tables (``rope_shift(..., tables="reference")``: elements that differ at all)."""
+    import numpy as np
+    import torch
+
+    from oracle import kvshift_oracle as orc
+
+    sl = small["slots"].numpy()
+    blk, off = sl // 16, sl % 16
+    beyond = differ_ref = total = 0
+    worst = 0
+    for layer, ref in enumerate(small["kv"]):
+        want = ref.view(torch.int16).numpy().view(np.uint16)[blk, :, off][..., :128]
+        exact = gpu_out["exact"][layer].view(torch.int16).numpy().view(np.uint16)[blk, :, off][..., :128]
+        refd = gpu_out["reference"][layer].view(torch.int16).numpy().view(np.uint16)[blk, :, off][..., :128]
+        u = orc.ulp_distance_bf16(exact, want)
+        beyond += int((u > 1).sum())
+        worst = max(worst, int(u.max()))
+        differ_ref += int((refd != want).sum())
+        total += want.size
+    return {"elements": total, "exact_tables_beyond_1ulp": beyond,
+            "exact_tables_fraction_beyond_1ulp": float(f"{beyond / total:.3e}"),
+            "exact_tables_max_ulp": worst, "reference_tables_elements_differing": differ_ref}
+
+
+def cpu_baseline(reps: int = 5, gpu_small: dict | None = None,
+                 small_gpu_out: dict | None = None) -> dict:
     """The reference torch shift path on the host CPU, on the headline workload itself:
     the Qwen3-14B multi-span shift (40 layers, 8 spans, 22,141 tokens), every layer and
     every span, read from the reference's flat store (shift_store.py:225-236, rows of a
@@ -194,7 +240,8 @@ def cpu_baseline(reps: int = 5, gpu_small: dict | None = None) -> dict:
         s0, d0, n, dl = int(s0), int(d0), int(n), int(dl)
         emb = torch_path.rope_emb_tables(dl, inv) if dl != 0 else None
         spans.append((s0, n, slot_map(table, d0, d0 + n, bs), emb))
-    best = float("inf")
+    load_before = _loadavg()
+    passes = []
     for i in range(reps + 1):
         t0 = time.perf_counter()
         for store, cache in zip(stores, caches):
@@ -202,7 +249,8 @@ def cpu_baseline(reps: int = 5, gpu_small: dict | None = None) -> dict:
                 torch_path.shift_into_paged(store[s0:s0 + n], cache, sl, bs, True, emb)
         dt = time.perf_counter() - t0
         if i:
-            best = min(best, dt)
+            passes.append(dt)
+    best = min(passes)
     tokens = int(lay.length.sum())
     moved = 2 * tokens * layers * heads * 2 * d * 2
     del stores, caches
@@ -210,19 +258,24 @@ def cpu_baseline(reps: int = 5, gpu_small: dict | None = None) -> dict:
     # the reference's own CPU-sized case
     small = W.qwen3_0_6b_cpu_shift()
     emb_small = torch_path.rope_emb_tables(small["delta"], small["inv_freq"])
-    best_small = float("inf")
+    passes_small = []
     for i in range(reps + 1):
         t0 = time.perf_counter()
         for src, kv in zip(small["src"], small["kv"]):
             torch_path.shift_into_paged(src, kv, small["slots"], 16, True, emb_small)
         dt = time.perf_counter() - t0
         if i:
-            best_small = min(best_small, dt)
+            passes_small.append(dt)
+    best_small = min(passes_small)
+    load_after = _loadavg()
     moved_small = 2 * sum(t.numel() * t.element_size() for t in small["src"])
     small_row = {
         "GB_s": round(moved_small / best_small / 1e9, 3),
         "ms_per_shift": round(best_small * 1e3, 2),
+        "passes_ms": _spread(passes_small),
     }
+    if small_gpu_out is not None:
+        small_row["k_vs_torch_path"] = _k_vs_torch_path(small, small_gpu_out)
     if gpu_small:
         small_row["hip"] = gpu_small
         small_row["hip_speedup_batched"] = round(best_small * 1e3 / gpu_small["batched_ms"], 1)
@@ -240,11 +293,14 @@ def cpu_baseline(reps: int = 5, gpu_small: dict | None = None) -> dict:
         f"(os.cpu_count() {cores['os_cpu_count']}, {cores['usable']} usable); "
         f"CPU: {_cpu_model()}",
         "ms_per_shift": round(best * 1e3, 2),
+        "passes_ms": _spread(passes),
+        "host_loadavg_1_5_15min": {"before": load_before, "after": load_after},
         "qwen3_0_6b_4096_tokens": small_row,
     }
 
 
-def qwen3_0_6b_hip(dev, steps: int, warmup: int, stream, iters: int = 5) -> dict:
+def qwen3_0_6b_hip(dev, steps: int, warmup: int, stream, iters: int = 5,
+                   keep_outputs: bool = False):
     """The Qwen3-0.6B-shaped shift the CPU baseline also times (28 layers, a flat store of
     4,096 tokens per layer, one span shifted by +37 into 259 of 512 seeded HND blocks),
     on the HIP path: one batched launch (HIP events on the launch stream, mean over
@@ -302,9 +358,23 @@ def qwen3_0_6b_hip(dev, steps: int, warmup: int, stream, iters: int = 5) -> dict
         "per_layer_loop_ms": round(best, 4),
         "per_layer_loop_GB_s": round(moved / (best / 1e3) / 1e9, 1),
     }
+    outputs = None
+    if keep_outputs:
+        # the caches as the per-layer loop left them (this package's tables), then the
+        # same loop with the reference's own torch fp32 tables built on the CPU, as the
+        # CPU torch path uses them; compared with that path after the CPU leg has run
+        torch.cuda.synchronize()
+        outputs = {"exact": [t.cpu() for t in kv]}
+        ref = rope_shift(delta, 128, wl["inv_freq"], "cpu", tables="reference")
+        ref = type(ref)(ref.delta, ref.cos.to(dev), ref.sgn.to(dev), ref.partner,
+                        ref.emb_cos, ref.emb_sin, ref.inv_freq, ref.rotary)
+        for s_, k_ in zip(src, kv):
+            scatter_shifted(s_, k_, slots, 16, True, ref)
+        torch.cuda.synchronize()
+        outputs["reference"] = [t.cpu() for t in kv]
     del src, kv, plan
     torch.cuda.empty_cache()
-    return out
+    return (out, outputs) if keep_outputs else out
 
 
 def reference_shape(dev, steps: int, warmup: int, stream) -> dict:
@@ -937,28 +1007,39 @@ def save_step(dev, steps: int, warmup: int) -> dict:
     names = [f"layer{i}" for i in range(layers)]
     kv = {name: torch.randn(blocks, heads, bs, 2 * d, dtype=torch.bfloat16, device=dev,
                             generator=gen) for name in names}
+    # the same cache in fp8 e4m3 (a save copies bytes: no K scale is involved)
+    kv8 = {name: (t.float() * 16).clamp(-448, 448).to(torch.float8_e4m3fn)
+           for name, t in kv.items()}
     table = np.random.default_rng(2).permutation(blocks).astype(np.int32)
     store = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
+    store8 = BlockShiftStore(budget_tokens=32768, device=str(dev), block_size=bs)
     saver = ShiftSaver(store, bs)
-    out = {"what": "ShiftSaver.save_all from an HND paged cache (40 layers, bf16) into a "
-           "BlockShiftStore session, block tables on the device; medians over steps"}
-    cases = {"full_prompt_29232_tokens": lambda: [Save.from_blocks("s", table, 0, n)],
-             "decode_step_1_token": lambda: [Save.from_blocks("s", table, n - 1, n)]}
-    for case, saves in cases.items():
+    saver8 = ShiftSaver(store8, bs)
+    out = {"what": "ShiftSaver.save_all from an HND paged cache (40 layers, bf16; fp8 e4m3 "
+           "where named) into a BlockShiftStore session, block tables on the device; "
+           "medians over steps"}
+    cases = {"full_prompt_29232_tokens": (kv, saver, lambda: [Save.from_blocks("s", table, 0, n)]),
+             "decode_step_1_token": (kv, saver,
+                                     lambda: [Save.from_blocks("s", table, n - 1, n)]),
+             "full_prompt_29232_tokens_fp8": (kv8, saver8,
+                                              lambda: [Save.from_blocks("s", table, 0, n)]),
+             "decode_step_1_token_fp8": (kv8, saver8,
+                                         lambda: [Save.from_blocks("s", table, n - 1, n)])}
+    for case, (kv_c, saver_c, saves) in cases.items():
         for _ in range(warmup):
-            saver.save_all(kv, saves())
+            saver_c.save_all(kv_c, saves())
         torch.cuda.synchronize()
         e2e, host = [], []
         for _ in range(steps):
             batch = saves()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            saver.save_all(kv, batch)
+            saver_c.save_all(kv_c, batch)
             t1 = time.perf_counter()
             torch.cuda.synchronize()
             e2e.append((time.perf_counter() - t0) * 1e3)
             host.append((t1 - t0) * 1e3)
-        plan = saver.last_plan
+        plan = saver_c.last_plan
         _, per = time_plan(plan, steps, warmup, torch.cuda.current_stream(dev))
         kms = float(np.mean(per))
         out[case] = {
@@ -991,7 +1072,7 @@ def save_step(dev, steps: int, warmup: int) -> dict:
             torch.cuda.synchronize()
             e2e.append((time.perf_counter() - t0) * 1e3)
         out[case] = {"tokens": 1, "ms_end_to_end": round(float(np.median(e2e)), 4)}
-    del store, kv, saver
+    del store, kv, saver, store8, kv8, saver8
     torch.cuda.empty_cache()
     return out
 
@@ -1126,9 +1207,11 @@ def main() -> int:
     small = cpu = None
     if not args.no_cpu_baseline:
         log("Qwen3-0.6B shift on the HIP path (the CPU baseline's small case)")
-        small = qwen3_0_6b_hip(dev, side_steps, args.warmup, stream)
+        small, small_out = qwen3_0_6b_hip(dev, side_steps, args.warmup, stream,
+                                          keep_outputs=True)
         log("cpu baseline (reference torch path on the host, the Qwen3-14B multi-span shift)")
-        cpu = cpu_baseline(gpu_small=small)
+        cpu = cpu_baseline(gpu_small=small, small_gpu_out=small_out)
+        del small_out
 
     tokens = int(bytes_step // (2 * 40 * 8 * 256 * 2))
     line = {
@@ -1173,6 +1256,10 @@ def main() -> int:
         "cpu_baseline": cpu,
         "qwen3_0_6b_shift_hip": small,
         "parity": f"{checked} sampled rows bit-identical to the oracle after timing",
+        # config 1's K (every shifted element, 28 layers) against the reference's torch
+        # path on the CPU: this package's tables and the reference's own
+        "k_vs_torch_path_qwen3_0_6b": None if cpu is None else
+        cpu["qwen3_0_6b_4096_tokens"].get("k_vs_torch_path"),
         **extra,
     }
     print(json.dumps(line), flush=True)
