@@ -678,6 +678,140 @@ def ceilings(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+CEILING_LIB = os.path.join(ROOT, "tests", "_lib", "libcopy_ceiling.so")
+
+
+def _ceiling_lib():
+    """The copy kernels of tests/hip/copy_ceiling.hip (built by ``build()``): benchmark
+    infrastructure, not the product library."""
+    import ctypes
+
+    if not os.path.exists(CEILING_LIB):
+        raise RuntimeError(f"{CEILING_LIB} is missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(CEILING_LIB)
+    i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+    lib.ceil_stream_copy.argtypes = [vp, vp, i64, i32, vp]
+    lib.ceil_paged_copy.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64, i32,
+                                    i32, i64, i64, i64, i64, i64, i64, vp]
+    return lib
+
+
+def _time_launch(launch, steps: int, stream) -> float:
+    """Median ms of ``launch()`` over ``steps`` launches, HIP events on ``stream``."""
+    import numpy as np
+    import torch
+
+    warm_up(launch)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record(stream)
+        launch()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return float(np.median([s_.elapsed_time(e) for s_, e in zip(starts, ends)]))
+
+
+def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
+    """Hand-written copies of the headline's bytes (tests/hip/copy_ceiling.hip), the
+    practical ceiling the shift kernel is held to:
+
+    * ``stream_copy_*``: one contiguous 3.63 GB buffer into another (the headline's
+      7.26 GB read once and written once), 16 bytes per thread, one-shot grid, XCD-aware
+      order, non-temporal loads; stores non-temporal (``nt``) or device-scope streaming
+      (``sc1 nt``, the shift kernel's stores).
+    * ``paged_copy_*``: the headline's 22,141 tokens x 40 layers from the session store's
+      blocks into the HND paged cache, through the headline's own shuffled block tables
+      (``shuffled``) or identity tables (``identity``), with no rotation and no token
+      metadata beyond the two block ids: bf16 from the store's K/V planes (64 KB blocks),
+      fp8 from its fused rows (32 KB blocks), as the headline and its fp8 twin read them.
+
+    Every copy is checked after timing: the stream copy whole, the paged copy on sampled
+    rows."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+
+    lib = _ceiling_lib()
+    st = ctypes.c_void_p(stream.cuda_stream)
+    runs = max(steps, 50)
+    out = {}
+    nbytes = 22141 * 40 * 8 * 256 * 2  # the headline's K and V bytes, read once
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    a = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev,
+                      generator=gen)
+    b = torch.empty_like(a)
+    for name, scope in (("stream_copy_nt", 0), ("stream_copy_sc1_nt", 1)):
+        b.zero_()
+
+        def launch(scope=scope):
+            if lib.ceil_stream_copy(a.data_ptr(), b.data_ptr(), nbytes, scope, st) != 0:
+                raise RuntimeError("ceil_stream_copy refused its arguments")
+
+        ms = _time_launch(launch, runs, stream)
+        if not torch.equal(a, b):
+            raise AssertionError(f"{name}: the copy differs from its source")
+        gbs = 2 * nbytes / (ms / 1e3) / 1e9
+        out[name] = {"bytes": 2 * nbytes, "ms": round(ms, 4), "GB_s": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    del a, b
+    torch.cuda.empty_cache()
+
+    n = 22141
+    rng = np.random.default_rng(0)
+    for dname, make in (("bf16", W.qwen3_14b_multispan), ("fp8", W.qwen3_14b_multispan_fp8)):
+        wl = make(dev)
+        eb = wl.dst.first.element_size()
+        heads, d, layers = wl.dst.heads, wl.dst.head_size, wl.layers
+        s_k, s_v, _, s_ready, _ = wl.src.device_tables(dev)
+        d_k, d_v, _, d_ready, _ = wl.dst.device_tables(dev)
+        torch.cuda.synchronize()
+        s_str = [x * eb for x in wl.src.strides]
+        d_str = [x * eb for x in wl.dst.strides]
+        src_blocks, dst_blocks = wl.src.first.shape[0], wl.dst.first.shape[0]
+        need = -(-n // 16)
+        tables = {
+            "shuffled": (np.asarray(wl.meta["src_table"], np.int32),
+                         np.asarray(wl.meta["dst_table"], np.int32)),
+            "identity": (np.arange(src_blocks, dtype=np.int32),
+                         np.arange(dst_blocks, dtype=np.int32)),
+        }
+        for tname, (st_np, dt_np) in tables.items():
+            st_dev = torch.from_numpy(st_np).to(dev)
+            dt_dev = torch.from_numpy(dt_np).to(dev)
+
+            def launch(st_dev=st_dev, dt_dev=dt_dev):
+                rc = lib.ceil_paged_copy(s_k, s_v, d_k, d_v, layers, st_dev.data_ptr(),
+                                         st_dev.numel(), src_blocks, dt_dev.data_ptr(),
+                                         dt_dev.numel(), dst_blocks, n, heads, d * eb,
+                                         *s_str, *d_str, st)
+                if rc != 0:
+                    raise RuntimeError(f"ceil_paged_copy returned {rc}")
+
+            ms = _time_launch(launch, runs, stream)
+            for _ in range(32):  # sampled rows: the destination row is the source row
+                pos, layer = int(rng.integers(n)), int(rng.integers(layers))
+                sb, db, off = int(st_np[pos // 16]), int(dt_np[pos // 16]), pos % 16
+                want = wl.src.fused(0, layer, (sb, off))  # [heads, 2D]
+                got = wl.dst.caches[0][layer][db, :, off]
+                if not torch.equal(want.contiguous().view(torch.uint8),
+                                   got.contiguous().view(torch.uint8)):
+                    raise AssertionError(f"paged_copy_{dname}_{tname}: row {pos} layer {layer}")
+            moved = 2 * n * layers * heads * 2 * d * eb
+            gbs = moved / (ms / 1e3) / 1e9
+            out[f"paged_copy_{dname}_{tname}"] = {
+                "bytes": moved, "ms": round(ms, 4), "GB_s": round(gbs, 1),
+                "frac_of_peak": round(gbs / PEAK_GBS, 4), "blocks_kb": 16 * heads * 2 * d * eb // 1024}
+            assert need <= len(st_np) and need <= len(dt_np)
+        del wl
+        torch.cuda.empty_cache()
+    return out
+
+
 def dst_layouts(dev, steps: int, warmup: int, stream) -> dict:
     """Informational: the headline shift into each paged-cache layout the connector
     takes -- fused HND (the headline), fused NHD, and K/V split into planes as
@@ -1190,6 +1324,8 @@ def main() -> int:
     if not args.no_ceilings:
         log("ceilings: elementwise copy, the headline with identity tables")
         extra["ceilings"] = ceilings(dev, side_steps, args.warmup, stream)
+        log("ceilings: hand-written stream and paged copies of the headline's bytes")
+        extra["ceilings"].update(copy_ceilings(dev, side_steps, args.warmup, stream))
     if not args.no_dst_layouts:
         log("destination layouts (fused HND / NHD, split K/V planes)")
         extra["dst_layouts"] = dst_layouts(dev, side_steps, args.warmup, stream)
