@@ -42,6 +42,7 @@ Prints one JSON line.  Also measured, in the same line:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -112,6 +113,7 @@ def spot_check(wl, rows: int = 96, seed: int = 0) -> int:
     rng = np.random.default_rng(seed)
     inv = wl.inv_freq.numpy()
     src_tab = wl.meta["src_table"]
+    sbs = wl.src.block_size
     dst_slots = wl.dst_index.numpy()
     spans = wl.spans
     checked = 0
@@ -121,7 +123,7 @@ def spot_check(wl, rows: int = 96, seed: int = 0) -> int:
         i = int(rng.integers(int(sp["n_tokens"])))
         layer = int(rng.integers(wl.layers))
         pos = int(sp["src_pos"]) + i
-        sblk, soff = int(src_tab[pos // 16]), pos % 16
+        sblk, soff = int(src_tab[pos // sbs]), pos % sbs
         slot = int(dst_slots[int(sp["dst_index"]) + i])
         dblk, doff = slot // 16, slot % 16
         src_row = wl.src.fused(0, layer, (sblk, soff)).cpu()  # [heads, 2D], K then V
@@ -491,6 +493,28 @@ def reference_loop(dev, iters: int = 5) -> dict:
             torch.cuda.synchronize()
             if i:
                 best_torch = min(best_torch, (time.perf_counter() - t0) * 1e3)
+        # and through the hand-written stream copy (tests/hip/copy_ceiling.hip, sc1 nt
+        # stores): the fastest 40-launch loop over these bytes found for this GPU
+        cl = _ceiling_lib()
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        nb = src[0].numel() * src[0].element_size()
+
+        def copy_loop():
+            for s, o in zip(src, outs):
+                if cl.ceil_stream_copy(s.data_ptr(), o.data_ptr(), nb, 1, st) != 0:
+                    raise RuntimeError("ceil_stream_copy refused its arguments")
+
+        warm_up(copy_loop)
+        best_copy = float("inf")
+        for i in range(iters + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            copy_loop()
+            torch.cuda.synchronize()
+            if i:
+                best_copy = min(best_copy, (time.perf_counter() - t0) * 1e3)
+        if not torch.equal(outs[-1], src[-1]):
+            raise AssertionError("stream copy loop output differs from its source")
         out[f"tokens_{n}"] = {
             "ms": round(best, 4),
             "GB_s": round(moved / (best / 1e3) / 1e9, 1),
@@ -499,6 +523,9 @@ def reference_loop(dev, iters: int = 5) -> dict:
             "host_enqueue_ms": round(host, 4),
             "torch_neg_loop_ms": round(best_torch, 4),
             "torch_neg_loop_GB_s": round(moved / (best_torch / 1e3) / 1e9, 1),
+            "stream_copy_loop_ms": round(best_copy, 4),
+            "stream_copy_loop_frac_of_peak": round(moved / (best_copy / 1e3) / 1e9 / PEAK_GBS, 4),
+            "frac_of_peak": round(moved / (best / 1e3) / 1e9 / PEAK_GBS, 4),
             "reference_rtx5090_ms": ref_ms,
         }
         del src, kv, slots, table, outs
@@ -577,6 +604,7 @@ def size_sweep(dev, steps: int, warmup: int, stream) -> dict:
 
     layers, heads, d, bs = 40, 8, 128, 16
     out = {}
+    cl = _ceiling_lib()
     for n in (512, 2048, 8192, 32768):
         gen = torch.Generator(device=dev)
         gen.manual_seed(n)
@@ -595,9 +623,21 @@ def size_sweep(dev, steps: int, warmup: int, stream) -> dict:
         _, per = time_plan(plan, max(steps, 50), warmup, stream)
         ms = float(np.median(per))
         gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+        # the same bytes through one launch of the hand-written stream copy, timed the
+        # same way (HIP events around each launch, median): the ceiling at this size
+        half = plan.algorithmic_bytes // 2
+        a = torch.empty(half, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        st = ctypes.c_void_p(stream.cuda_stream)
+        cms = _time_launch(lambda: cl.ceil_stream_copy(a.data_ptr(), b.data_ptr(), half, 1, st),
+                           max(steps, 50), stream)
         out[f"tokens_{n}"] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
                               "frac_of_peak": round(gbs / PEAK_GBS, 4),
-                              "us_per_token": round(ms * 1e3 / n, 5)}
+                              "us_per_token": round(ms * 1e3 / n, 5),
+                              "stream_copy_ms": round(cms, 4),
+                              "stream_copy_frac_of_peak": round(
+                                  plan.algorithmic_bytes / (cms / 1e3) / 1e9 / PEAK_GBS, 4)}
+        del a, b
         del src, kv, plan
         torch.cuda.empty_cache()
     return out
@@ -883,6 +923,39 @@ def src_layouts(dev, steps: int, warmup: int, stream) -> dict:
     return out
 
 
+def src_block_sizes(dev, steps: int, warmup: int, stream) -> dict:
+    """Tokens per session-store block, the store's own choice (the destination keeps
+    vLLM's 16-token blocks): the Qwen3-14B multi-span shift in bf16 and fp8, and its fp8
+    one-KV-head share (tensor parallelism 8), from store blocks of 16, 32 and 64 tokens
+    through shuffled tables; the launches alternate over 5 rounds (the best round's
+    median of each), and sampled rows of each are checked against the oracle."""
+    import torch
+
+    from marathon_amd import workloads as W
+
+    out = {}
+    cases = (("bf16", W.qwen3_14b_multispan, {}), ("fp8", W.qwen3_14b_multispan_fp8, {}),
+             ("fp8_1_head", W.qwen3_14b_multispan_fp8, {"heads": 1}))
+    for name, make, kw in cases:
+        wls = {blk: make(dev, src_block=blk, **kw) for blk in (16, 32, 64)}
+        plans = {blk: wl.plan() for blk, wl in wls.items()}
+        for plan in plans.values():
+            warm_up(lambda: plan.launch(stream.cuda_stream))
+        best = _ab(plans, max(steps, 50), warmup, stream, rounds=5)
+        for blk, ms in best.items():
+            gbs = plans[blk].algorithmic_bytes / (ms / 1e3) / 1e9
+            row = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
+                   "frac_of_peak": round(gbs / PEAK_GBS, 4),
+                   "store_block_kb": blk * wls[blk].dst.heads * 2 * 128
+                   * wls[blk].dst.first.element_size() // 1024}
+            if name == "bf16":
+                row["rows_checked"] = spot_check(wls[blk], rows=32, seed=blk)
+            out[f"{name}_store_block_{blk}"] = row
+        del wls, plans
+        torch.cuda.empty_cache()
+    return out
+
+
 def _same_output(a_plan, b_plan, caches) -> bool:
     """Run two plans of one workload into zeroed caches; whether every byte matches."""
     import torch
@@ -916,10 +989,13 @@ def _ab(plans: dict, steps: int, warmup: int, stream, rounds: int = 3) -> dict:
 def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
     """A/B of the plan options, each pair on one workload with byte-identical output.
 
-    * ``record_order``: the two-launch path's token records in span order (the default)
-      against ``order="dst_page"`` (records sorted by the 2 MB page of the destination
-      row, which costs an ordered plan pass and two more small launches), on the fp8 and
-      bf16 Qwen3-14B multi-span shifts and one GPU's fp8 share at 1 KV head.
+    * ``record_order``: the two-launch path's token records in span order against
+      destination-page order (records sorted by the 2 MB page of the destination row),
+      sorted on the host (``dst_page``: the plan's ``token_order``, no extra launch) and
+      on the device (``dst_page_device``: an ordered plan pass and one more small
+      launch), on the fp8 and bf16 Qwen3-14B multi-span shifts, the fp8 one from 64-token
+      store blocks, and one GPU's fp8 share at 1 KV head; ``host_order_ms`` is what
+      computing the host order adds to building the plan.
     * ``direct``: the single-launch path (token prefix and rotation tables from the
       host, no plan pass or workspace) against the two-launch path, for one span of
       16 to 2,048 tokens x 40 layers (flat store -> HND paged cache through shuffled
@@ -937,22 +1013,36 @@ def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
     out = {"record_order": {}, "direct": {"default_max_token_layers":
                                           S.DIRECT_MAX_TOKEN_LAYERS}}
     for name, make in (("qwen3_14b_multispan_fp8", lambda: W.qwen3_14b_multispan_fp8(dev)),
+                       ("qwen3_14b_multispan_fp8_store_block_64",
+                        lambda: W.qwen3_14b_multispan_fp8(dev, src_block=64)),
                        ("qwen3_14b_multispan_bf16", lambda: W.qwen3_14b_multispan(dev)),
                        ("qwen3_14b_multispan_fp8_1_head",
                         lambda: W.qwen3_14b_multispan_fp8(dev, heads=1))):
         log(f"record order A/B: {name}")
         wl = make()
+        t0 = time.perf_counter()
+        wl.plan(direct=False, order="none")
+        t1 = time.perf_counter()
+        wl.plan(direct=False, order="dst_page")
+        t2 = time.perf_counter()
         plans = {"none": wl.plan(direct=False, order="none"),
-                 "dst_page": wl.plan(direct=False, order="dst_page")}
-        same = _same_output(plans["none"], plans["dst_page"], wl.dst.caches[0])
+                 "dst_page": wl.plan(direct=False, order="dst_page"),
+                 "dst_addr": wl.plan(direct=False, order="dst_addr"),
+                 "dst_page_device": wl.plan(direct=False, order="dst_page_device")}
+        assert plans["dst_page"].order == "dst_page_host"
+        same = all(_same_output(plans["none"], plans[k], wl.dst.caches[0])
+                   for k in ("dst_page", "dst_addr", "dst_page_device"))
         warm_up(lambda: plans["none"].launch(stream.cuda_stream))
-        ms = _ab(plans, max(steps, 30), warmup, stream)
+        ms = _ab(plans, max(steps, 30), warmup, stream, rounds=4)
         gb = plans["none"].algorithmic_bytes
         out["record_order"][name] = {
             **{f"{k}_ms": round(v, 4) for k, v in ms.items()},
             **{f"{k}_frac_of_peak": round(gb / (v / 1e3) / 1e9 / PEAK_GBS, 4)
                for k, v in ms.items()},
             "dst_page_gain_pct": round(100 * (ms["none"] / ms["dst_page"] - 1), 2),
+            "dst_addr_gain_pct": round(100 * (ms["none"] / ms["dst_addr"] - 1), 2),
+            "dst_page_device_gain_pct": round(100 * (ms["none"] / ms["dst_page_device"] - 1), 2),
+            "host_order_ms": round((t2 - t1 - (t1 - t0)) * 1e3, 3),
             "bit_identical": same,
         }
         del wl, plans
@@ -1234,6 +1324,8 @@ def main() -> int:
                     help="skip the headline shift into the other paged-cache layouts")
     ap.add_argument("--no-src-layouts", action="store_true",
                     help="skip the headline shift from the store's other block layout")
+    ap.add_argument("--no-src-block-sizes", action="store_true",
+                    help="skip the A/B of 16-, 32- and 64-token store blocks")
     ap.add_argument("--no-connector-step", action="store_true",
                     help="skip the end-to-end connector load and save step timings")
     ap.add_argument("--no-plan-variants", action="store_true",
@@ -1248,7 +1340,7 @@ def main() -> int:
     if args.only:
         keep = {x.strip() for x in args.only.split(",") if x.strip()}
         sections = {"reference_shape", "reference_loop", "other_workloads", "tp_shares",
-                    "size_sweep", "ceilings", "dst_layouts", "src_layouts",
+                    "size_sweep", "ceilings", "dst_layouts", "src_layouts", "src_block_sizes",
                     "connector_step", "plan_variants", "cpu_baseline"}
         if keep - sections - {"headline"}:  # "headline": the headline line alone
             ap.error(f"--only: unknown sections {sorted(keep - sections)}")
@@ -1332,6 +1424,9 @@ def main() -> int:
     if not args.no_src_layouts:
         log("store block layouts (K/V planes, fused rows), bf16 and fp8")
         extra["src_layouts"] = src_layouts(dev, side_steps, args.warmup, stream)
+    if not args.no_src_block_sizes:
+        log("store block sizes (16, 32, 64 tokens), bf16, fp8, fp8 one head")
+        extra["src_block_sizes"] = src_block_sizes(dev, side_steps, args.warmup, stream)
     if not args.no_connector_step:
         log("connector load step (block store, device-side slots)")
         extra["connector_step"] = connector_step(dev, side_steps, args.warmup)

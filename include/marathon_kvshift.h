@@ -176,6 +176,14 @@ typedef struct mkv_side {
  *                  together touch few destination pages.  The workspace then needs
  *                  MKV_ORDER_EXTRA_BYTES(total_tokens) more bytes.  Results are the same
  *                  bytes either way.  Ignored on the direct path.
+ *   token_order  : optional device int32 [total_tokens], the same kind of order chosen
+ *                  by the caller, with no extra launch: on the two-launch path the plan
+ *                  pass resolves record i from token token_order[i] (tokens numbered in
+ *                  span order, 0 <= token_order[i] < total_tokens), and the shift moves
+ *                  the records in that order.  A permutation moves every token once and
+ *                  writes the same bytes as span order; an entry out of range raises
+ *                  MKV_FLAG_SPAN and moves nothing.  NULL = span order.  Not together
+ *                  with MKV_ORDER_DST_PAGE (MKV_ERR_ARG).  Ignored on the direct path.
  */
 typedef struct mkv_shift_desc {
   const mkv_span_t* spans;
@@ -197,6 +205,7 @@ typedef struct mkv_shift_desc {
   const float* span_tables;
   int32_t order;
   int32_t reserved;
+  const int32_t* token_order;
 } mkv_shift_desc_t;
 
 /*
@@ -289,7 +298,7 @@ const char* mkv_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. */
 int32_t mkv_abi_version(void);
-#define MKV_ABI_VERSION ((3 << 16) | 2)
+#define MKV_ABI_VERSION ((3 << 16) | 3)
 
 #ifdef __cplusplus
 }

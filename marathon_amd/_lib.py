@@ -45,7 +45,7 @@ MKV_MAX_HEAD_SIZE = 512
 MKV_DIRECT_MAX_SPANS = 63
 MKV_SMALL_MAX_SPANS = 8
 MKV_SMALL_MAX_INDEX = 64
-MKV_ABI_VERSION = (3 << 16) | 2
+MKV_ABI_VERSION = (3 << 16) | 3
 MKV_ORDER_NONE = 0
 MKV_ORDER_DST_PAGE = 1
 MKV_NOALLOC_SCRATCH_BYTES = 16 << 20
@@ -122,7 +122,7 @@ class Side(ctypes.Structure):
 
 
 class ShiftDesc(ctypes.Structure):
-    """mkv_shift_desc_t (280 bytes)."""
+    """mkv_shift_desc_t (288 bytes)."""
 
     _fields_ = [
         ("spans", ctypes.c_void_p),
@@ -144,10 +144,11 @@ class ShiftDesc(ctypes.Structure):
         ("span_tables", ctypes.c_void_p),
         ("order", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("token_order", ctypes.c_void_p),
     ]
 
 
-assert ctypes.sizeof(Side) == 88 and ctypes.sizeof(ShiftDesc) == 280
+assert ctypes.sizeof(Side) == 88 and ctypes.sizeof(ShiftDesc) == 288
 
 
 class KVShiftError(RuntimeError):

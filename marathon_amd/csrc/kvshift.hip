@@ -127,6 +127,12 @@
 #ifndef MKV_XCDS
 #define MKV_XCDS 8
 #endif
+// Which rows a wave's passes take when it makes more than one (fp8, fp32): 0 = pass u of
+// wave w takes the tile's row group w + waves * u (the waves interleave); 1 = w * passes + u
+// (a wave's passes take adjacent row groups: for 8 heads, adjacent tokens).
+#ifndef MKV_PASS_MAJOR
+#define MKV_PASS_MAJOR 0
+#endif
 
 namespace {
 
@@ -217,6 +223,7 @@ struct PlanParams {
   uint32_t* order_hist;  // ordered: [gridDim.x][kOrderBuckets] page counts per workgroup
   int64_t order_chunk;   // ordered: tokens per workgroup (contiguous)
   int32_t order_shift;   // ordered: destination offset >> this = bucket
+  const int32_t* token_order;  // record i resolves token token_order[i] (NULL: token i)
   int32_t* err;
   int64_t total_tokens;
   int32_t n_spans;
@@ -568,22 +575,26 @@ __device__ __forceinline__ uint32_t order_bucket(const TokRec& r, int shift) {
   return page < kOrderBuckets ? static_cast<uint32_t>(page) : kOrderBuckets - 1;
 }
 
-// This lane's C cos / signed-sin values of a span's rotation, computed as the plan pass
-// computes its tables (fp32 angle, double-precision sincos, rounded to fp32).
-template <int C>
-__device__ __forceinline__ void lane_tables(int delta, const float* inv_freq, int rotary, int j,
-                                            float* cs, float* sg) {
+// cos and sin of frequency f's angle for one delta: the fp32 angle fl32(delta * inv_freq[f])
+// (shift_kernels.py:73), its sine and cosine evaluated in double precision and rounded
+// once to fp32.  The one routine behind every table the device makes (the plan pass and
+// the small path), so they hold the same bits.
+__device__ __forceinline__ void angle_cos_sin(int delta, float inv_freq_f, float& c, float& s) {
+  const float ang = static_cast<float>(delta) * inv_freq_f;
+  double sd, cd;
+  sincos(static_cast<double>(ang), &sd, &cd);
+  c = static_cast<float>(cd);
+  s = static_cast<float>(sd);
+}
+
+// A span's table in the layout every path reads: [2][rotary], the cos of each element's
+// frequency, then its signed sine (-sin on the first half, +sin on the second).
+__device__ __forceinline__ void put_table(float* t, int rotary, int f, float c, float s) {
   const int half = rotary / 2;
-#pragma unroll
-  for (int e = 0; e < C; ++e) {
-    const int i = j * C + e;
-    const int f = i < half ? i : i - half;
-    const float ang = static_cast<float>(delta) * inv_freq[f];
-    double sd, cd;
-    sincos(static_cast<double>(ang), &sd, &cd);
-    cs[e] = static_cast<float>(cd);
-    sg[e] = i < half ? -static_cast<float>(sd) : static_cast<float>(sd);
-  }
+  t[f] = c;
+  t[f + half] = c;
+  t[rotary + f] = -s;
+  t[rotary + f + half] = s;
 }
 
 // --------------------------------------------------------------------- plan kernel
@@ -661,16 +672,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
   for (int64_t idx = gtid; idx < pairs; idx += gstride) {
     const int s = static_cast<int>(idx / half);
     const int f = static_cast<int>(idx - static_cast<int64_t>(s) * half);
-    const float ang = static_cast<float>(p.spans[s].delta) * p.inv_freq[f];
-    double sd, cd;
-    sincos(static_cast<double>(ang), &sd, &cd);
-    const float c = static_cast<float>(cd);
-    const float sn = static_cast<float>(sd);
-    float* t = p.tables + static_cast<int64_t>(s) * 2 * p.rotary;
-    t[f] = c;
-    t[f + half] = c;
-    t[p.rotary + f] = -sn;
-    t[p.rotary + f + half] = sn;
+    float c, sn;
+    angle_cos_sin(p.spans[s].delta, p.inv_freq[f], c, sn);
+    put_table(p.tables + static_cast<int64_t>(s) * 2 * p.rotary, p.rotary, f, c, sn);
   }
 
   // token records: grid-stride, or (ordered) one contiguous chunk per workgroup with
@@ -694,18 +698,27 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
     r.delta = 0;
     r.src_base = 0;
     r.dst_base = 0;
-    if (g < actual) {
-      int lo = 0, hi = n;  // largest s with s_pre[s] <= g; then s_pre[s + 1] > g
+    // the token this record resolves: the caller's order, or span order
+    int64_t tok = g;
+    if (p.token_order != nullptr) {
+      tok = p.token_order[g];
+      if (tok < 0 || tok >= p.total_tokens) {
+        if (p.err != nullptr) atomicOr(p.err, MKV_FLAG_SPAN);
+        tok = actual;  // resolves nothing
+      }
+    }
+    if (tok < actual) {
+      int lo = 0, hi = n;  // largest s with s_pre[s] <= tok; then s_pre[s + 1] > tok
       while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (s_pre[mid] <= g) lo = mid;
+        if (s_pre[mid] <= tok) lo = mid;
         else hi = mid;
       }
       const mkv_span_t sp = p.spans[lo];
       const bool groups_ok = sp.src_group >= 0 && sp.src_group < p.src.groups &&
                              sp.dst_group >= 0 && sp.dst_group < p.dst.groups;
       if (groups_ok) {
-        const int64_t i = g - s_pre[lo];
+        const int64_t i = tok - s_pre[lo];
         int64_t s_cap = p.src.num_slots, d_cap = p.dst.num_slots;
         if (p.src.group_slots != nullptr) s_cap = p.src.group_slots[sp.src_group];
         if (p.dst.group_slots != nullptr) d_cap = p.dst.group_slots[sp.dst_group];
@@ -876,6 +889,19 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   if (left <= 0) return;  // padding workgroups of the XCD-aware grid
   const int ntok = static_cast<int>(left < p.tile_tokens ? left : p.tile_tokens);
   const int nrows = ntok * H;
+  // small: the spans of the workgroup's tokens [g0, g0 + ntok), whose rotation tables the
+  // workgroup computes together into LDS ([span - small_lo][2][rotary])
+  float* small_tab = nullptr;
+  int small_lo = 0, small_hi = 0;
+  if constexpr (SMALL) {
+    extern __shared__ float small_lds[];
+    small_tab = small_lds;
+#pragma unroll
+    for (int k = 0; k < MKV_SMALL_MAX_SPANS; ++k) {
+      if (k < p.n_spans && q->starts[k] <= g0) small_lo = k;
+      if (k < p.n_spans && q->starts[k] <= g0 + ntok - 1) small_hi = k;
+    }
+  }
   // per-lane constant part of the addresses (UNIFORM: lane head = pass head + row_in_wave)
   const uint32_t s_lane = UNIFORM ? static_cast<uint32_t>(row_in_wave) *
                                             static_cast<uint32_t>(p.src_hstride) + chunk_off
@@ -944,6 +970,28 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     }
   }
 
+    if constexpr (SMALL) {
+    // the workgroup computes the tables of its spans together (at most one cos/sin pair
+    // per thread for a one-span step) into LDS, with the routine of the plan pass, so
+    // every path holds the same table bits.  Done before the data loads: evaluated
+    // beside them it kept the loads' registers live through the double-precision sine
+    // and cosine (133 against 93 VGPRs for fp8).
+    if (p.rotary > 0) {
+      const int half = p.rotary / 2;
+      const int pairs = (small_hi - small_lo + 1) * half;
+      for (int idx = tid; idx < pairs; idx += kThreads) {
+        const int k = idx / half;
+        const int f = idx - k * half;
+        const int dl = q->spans[small_lo + k].delta;
+        if (dl != 0) {
+          float c, sn;
+          angle_cos_sin(dl, p.inv_freq[f], c, sn);
+          put_table(small_tab + k * 2 * p.rotary, p.rotary, f, c, sn);
+        }
+      }
+      __syncthreads();
+    }
+  }
   for (int r0 = 0; r0 < nrows; r0 += kWaves * U * rpw) {
     // ---- phase A: where each pass reads and writes (uniform when UNIFORM).  All token
     // metadata is fetched first, then all base addresses, so the workgroup pays two
@@ -960,7 +1008,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     int sb_u[U], db_u[U];      // the (group, layer 0) rows of the base tables
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row0 = r0 + (wave + kWaves * u) * rpw;
+      const int row0 = r0 + (MKV_PASS_MAJOR ? wave * U + u : wave + kWaves * u) * rpw;
       const int r = UNIFORM ? row0 : row0 + row_in_wave;
       const int rr = r < nrows ? r : nrows - 1;  // clamp: metadata reads stay in range
       const int t = H == 1 ? rr
@@ -1244,7 +1292,13 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         if constexpr (BATCHED) {
           if (span_u[u] != cur_span) {
             if constexpr (SMALL) {
-              lane_tables<C>(delta_u[u], p.inv_freq, p.rotary, j, cs, sg);
+              // the workgroup's own table, computed into LDS in phase B
+              const float* tb = small_tab + (span_u[u] - small_lo) * 2 * p.rotary;
+#pragma unroll
+              for (int e = 0; e < C; ++e) {
+                cs[e] = tb[j * C + e];
+                sg[e] = tb[p.rotary + j * C + e];
+              }
             } else {
               const float* tb = p.tables + static_cast<int64_t>(span_u[u]) * 2 * p.rotary;
 #pragma unroll
@@ -1627,6 +1681,9 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   if (d->src.k_base == nullptr || d->src.v_base == nullptr || d->dst.k_base == nullptr ||
       d->dst.v_base == nullptr)
     return fail(MKV_ERR_ARG, "NULL base-address table");
+  if (d->token_order != nullptr && d->order != MKV_ORDER_NONE)
+    return fail(MKV_ERR_ARG, "token_order and order %d together: one order or the other",
+                d->order);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t tiles = (d->total_tokens + g.tile_tokens - 1) / g.tile_tokens;
   if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "total_tokens too large");
@@ -1709,6 +1766,7 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   pp.inv_freq = d->inv_freq;
   pp.tables = tables;
   pp.recs = recs;
+  pp.token_order = d->token_order;
   pp.err = d->error_flags;
   pp.total_tokens = d->total_tokens;
   pp.n_spans = d->n_spans;
@@ -1761,9 +1819,11 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
 template <int DT>
 int launch_small(const SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
   tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
+  // LDS for the rotation tables of the spans one workgroup may touch
+  const size_t lds = static_cast<size_t>(a.p.n_spans) * 2 * a.p.rotary * sizeof(float);
   hipLaunchKernelGGL(shift_small_kernel<DT>,
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layers)),
-                     dim3(kThreads), 0, stream, a);
+                     dim3(kThreads), lds, stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
   return MKV_OK;

@@ -207,27 +207,27 @@ STORE_LAYOUTS = ("planes", "fused")
 
 
 def store_blocks(blocks: int, heads: int, dtype, gen, device, k_scale=None, v_scale=None,
-                 layout: str = "planes") -> torch.Tensor:
-    """One layer of a session store: ``blocks`` blocks of N(0, 1) K and V (fp8: divided
-    by the layer's K and V scales) in ``layout``."""
+                 layout: str = "planes", block: int = BLOCK) -> torch.Tensor:
+    """One layer of a session store: ``blocks`` blocks of ``block`` tokens of N(0, 1) K
+    and V (fp8: divided by the layer's K and V scales) in ``layout``."""
     if layout not in STORE_LAYOUTS:
         raise ValueError(f"store layout {layout!r}")
-    plane = (blocks, BLOCK, heads, HEAD_SIZE)
+    plane = (blocks, block, heads, HEAD_SIZE)
     if dtype != torch.float8_e4m3fn:
         if layout == "planes":
-            return _randn_cache((blocks, 2, BLOCK, heads, HEAD_SIZE), dtype, gen, device)
-        return _randn_cache(_paged(blocks, "nhd", heads), dtype, gen, device)
+            return _randn_cache((blocks, 2, block, heads, HEAD_SIZE), dtype, gen, device)
+        return _randn_cache((blocks, block, heads, 2 * HEAD_SIZE), dtype, gen, device)
     k = _randn_cache(plane, dtype, gen, device, k_scale)
     v = _randn_cache(plane, dtype, gen, device, v_scale)
     return torch.stack((k, v), dim=1) if layout == "planes" else torch.cat((k, v), dim=-1)
 
 
-def store_cache_set(groups: list, layout: str = "planes") -> CacheSet:
+def store_cache_set(groups: list, layout: str = "planes", block: int = BLOCK) -> CacheSet:
     """A :class:`CacheSet` over ``groups[group][layer]`` tensors from :func:`store_blocks`."""
     if layout == "planes":
-        return CacheSet([[t[:, 0] for t in row] for row in groups], "nhd", BLOCK,
+        return CacheSet([[t[:, 0] for t in row] for row in groups], "nhd", block,
                         v_caches=[[t[:, 1] for t in row] for row in groups])
-    return CacheSet(groups, "nhd", BLOCK)
+    return CacheSet(groups, "nhd", block)
 
 
 def single_session_workload(
@@ -243,17 +243,19 @@ def single_session_workload(
     dst_fill: str = "zeros",
     heads: int = HEADS,
     src_layout: str | None = None,
+    src_block: int = BLOCK,
 ) -> Workload:
     """One session's store (blocks in ``src_layout``, via a shuffled table) -> one HND
     paged cache via a slot mapping: the single-span and multi-span workloads, bf16 or
     fp8.  ``heads`` below 8 is one GPU's share of the KV heads under tensor
     parallelism.  ``src_layout``: ``"planes"`` or ``"fused"`` (default: the block store's
-    layout for ``dtype``)."""
+    layout for ``dtype``).  ``src_block``: tokens per store block (the store's own
+    choice; the destination keeps vLLM's 16)."""
     src_layout = src_layout or store_layout(dtype)
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
-    src_blocks = -(-layout.src_history // BLOCK)
+    src_blocks = -(-layout.src_history // src_block)
     dst_need = -(-layout.dst_history // BLOCK)
     dst_pool = dst_need + spare_blocks
     src_table = rng.permutation(src_blocks).astype(np.int32)
@@ -267,7 +269,8 @@ def single_session_workload(
         fp8 = dtype == torch.float8_e4m3fn
         src_caches.append(store_blocks(src_blocks, heads, dtype, gen, device,
                                        k_scale[layer] if fp8 else None,
-                                       v_scale[layer] if fp8 else None, src_layout))
+                                       v_scale[layer] if fp8 else None, src_layout,
+                                       src_block))
         if dst_fill == "random" and dtype != torch.float8_e4m3fn:
             dst_caches.append(_randn_cache(_paged(dst_pool, "hnd", heads), dtype, gen, device))
         else:
@@ -282,7 +285,7 @@ def single_session_workload(
     return Workload(
         name,
         spans,
-        store_cache_set([src_caches], src_layout),
+        store_cache_set([src_caches], src_layout, src_block),
         CacheSet([dst_caches], "hnd", BLOCK),
         "table",
         torch.from_numpy(src_table),

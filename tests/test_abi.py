@@ -386,3 +386,67 @@ def test_rope_shift_reference_tables_are_the_reference_construction():
             assert np.array_equal(exact.emb_sin.numpy()[: rotary // 2], s)
     with pytest.raises(ValueError, match="tables"):
         rope_shift(1, 128, inv, "cpu", tables="torch")
+
+
+def test_token_order_and_device_order_are_refused_together():
+    """The caller's token order and the device's page sort are two ways to order one
+    shift; a descriptor asking for both is refused before anything is enqueued."""
+    lib = _lib.lib()
+    d = _lib.ShiftDesc()
+    d.heads, d.head_size, d.rotary, d.dtype, d.layers = 8, 128, 128, _lib.MKV_BF16, 2
+    d.inv_freq = 1 << 21
+    d.spans = 1 << 22
+    d.n_spans, d.total_tokens = 1, 16
+    for side in (d.src, d.dst):
+        side.k_base, side.v_base = 1 << 24, 1 << 25
+        side.mode, side.block_size, side.groups = _lib.MKV_ADDR_FLAT, 1, 1
+    d.order = _lib.MKV_ORDER_DST_PAGE
+    d.token_order = 1 << 23
+    assert lib.mkv_shift_spans(ctypes.byref(d), None) == _lib.MKV_ERR_ARG
+    assert b"token_order" in lib.mkv_last_error()
+
+
+def test_host_page_order_matches_a_brute_force_restatement():
+    """``spans.dst_page_order`` (the pages ShiftPlan sorts by on the host) equals a
+    per-token restatement of the device's bucket rule, for slots, block tables and a flat
+    destination; the resulting order is a stable permutation."""
+    from marathon_amd.spans import CacheSet, dst_page_order, span_array
+
+    rng = np.random.default_rng(5)
+    blocks, bs = 3000, 16  # 3,000 x 64 KB: wider than 256 pages of 2 MB
+    hnd = CacheSet([torch.zeros(blocks, 8, bs, 256, dtype=torch.bfloat16)], "hnd", bs)
+    bstride, ostride = 8 * bs * 256 * 2, 256 * 2
+    extent = (blocks + 1) * bstride
+    shift = 21
+    while (extent >> shift) >= 256:
+        shift += 1
+    table = rng.permutation(blocks).astype(np.int32)
+    slots = rng.permutation(blocks * bs)[:900].astype(np.int64)
+    spans = span_array([(0, 5, 0, 0, 400, 7, 0, 0), (0, 900, 0, 400, 500, -3, 0, 0)])
+    want_slots, want_table = [], []
+    for sp in spans:
+        for i in range(int(sp["n_tokens"])):
+            s = int(slots[int(sp["dst_index"]) + i])
+            want_slots.append(min(((s // bs) * bstride + (s % bs) * ostride) >> shift, 255))
+            pos = int(sp["dst_pos"]) + i
+            b = int(table[pos // bs])  # the table case below uses dst_index 0
+            want_table.append(min((b * bstride + (pos % bs) * ostride) >> shift, 255))
+    got = dst_page_order(spans, hnd, "slots", slots)
+    assert got.dtype == np.uint8 and got.tolist() == want_slots
+    spans_t = spans.copy()
+    spans_t["dst_index"] = 0
+    assert dst_page_order(spans_t, hnd, "table", table).tolist() == want_table
+    perm = np.argsort(got, kind="stable")
+    assert sorted(perm.tolist()) == list(range(got.size))
+    assert all(got[perm][:-1] <= got[perm][1:])
+    flat = CacheSet([torch.zeros(5000, 8, 256, dtype=torch.bfloat16)], "flat")
+    fl = dst_page_order(span_array([(0, 10, 0, 0, 4000, 1, 0, 0)]), flat, "flat", None)
+    fext = (5000 + 1) * 8 * 256 * 2
+    fshift = 21
+    while (fext >> fshift) >= 256:
+        fshift += 1
+    assert fl.tolist() == [min(((10 + i) * 8 * 256 * 2) >> fshift, 255) for i in range(4000)]
+    # an out-of-range slot lands in bucket 0 (the device flags and skips it)
+    bad = slots.copy()
+    bad[3] = blocks * bs + 7
+    assert dst_page_order(spans, hnd, "slots", bad)[3] == 0

@@ -79,7 +79,7 @@ def _check(gpu, spans, src, dst, src_index, dst_index, **plan_kw):
     return plan
 
 
-@pytest.mark.parametrize("order", ["none", "dst_page"])
+@pytest.mark.parametrize("order", ["none", "dst_page", "dst_page_device"])
 def test_more_spans_than_one_descriptor_takes(gpu, order):
     n = _lib.MKV_MAX_SPANS + 905
     print(f"case {n} spans in one plan (several launches), order={order}", flush=True)

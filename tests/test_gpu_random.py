@@ -184,7 +184,8 @@ def _build(c, gpu):
                        src_mode="flat" if c["src_layout"] == "flat" else "table",
                        src_index=src_index, dst_mode=c["dst_mode"], dst_index=dst_index,
                        k_scale=k_scale, direct=direct, order=order)
-             for direct, order in ((False, "none"), (False, "dst_page"), (True, None))]
+             for direct, order in ((False, "none"), (False, "dst_page"),
+                                   (False, "dst_page_device"), (True, None))]
     src_o = oracle_side(src_cs, "flat" if c["src_layout"] == "flat" else "table", src_index)
     dst_o = oracle_side(dst_cs, c["dst_mode"], dst_index)
     return plans, dst_cs, spans, src_o, dst_o, inv, k_scale
@@ -192,10 +193,11 @@ def _build(c, gpu):
 
 @pytest.mark.parametrize("seed", range(max(48, _EXTRA)))
 def test_random_batched_shift_matches_oracle(gpu, seed):
-    """Each case runs three times from the same starting caches: the two-launch path
-    (plan pass and workspace) in span order and in destination-page order, and the
-    direct single-launch path, where the case is eligible for it (up to 63 spans,
-    power-of-two blocks, heads a multiple of a wave's rows)."""
+    """Each case runs four times from the same starting caches: the two-launch path
+    (plan pass and workspace) in span order, in destination-page order sorted on the host
+    (``token_order``) and sorted on the device, and the direct single-launch path, where
+    the case is eligible for it (up to 63 spans, power-of-two blocks, heads a multiple of
+    a wave's rows)."""
     c = _case(seed)
     desc = {k: (str(v) if k == "dtype" else v) for k, v in c.items() if k != "rng"}
     print(f"case random {desc}", flush=True)

@@ -627,7 +627,7 @@ def test_page_order_over_a_destination_wider_than_256_pages(gpu):
     src_o = oracle_side(CacheSet([src], "flat"), "flat", None)
     dst_o = oracle_side(CacheSet([kv], "hnd", bs), "slots", dst_slots)
     orc.shift_spans(oracle_spans(span_array(rows)), src_o, dst_o, inv_freq().numpy(), "bf16")
-    for order in ("none", "dst_page"):
+    for order in ("none", "dst_page", "dst_page_device"):
         kv[0].zero_()
         plan = ShiftPlan(span_array(rows), CacheSet([src], "flat"), CacheSet([kv], "hnd", bs),
                          inv_freq=inv_freq(), src_mode="flat", dst_mode="slots",
@@ -681,3 +681,53 @@ def test_direct_path_above_the_wide_threshold(gpu, dtype, d, layers):
     assert int(flags.item()) == 0
     for layer in range(layers):
         assert np.array_equal(bits(kv[layer]), dst_o.caches[0][layer]), f"layer {layer}"
+
+
+def test_caller_token_order(gpu):
+    """``mkv_shift_desc_t.token_order``: the plan pass resolves record i from token
+    token_order[i].  A reversed order writes the oracle's bytes; an entry out of range
+    raises MKV_FLAG_SPAN and leaves that record empty (its token is not moved, and every
+    other row is still the oracle's or untouched)."""
+    import ctypes
+
+    from marathon_amd import _lib, workloads as W
+    from marathon_amd.shift_kernels import current_stream
+
+    print("case caller token order", flush=True)
+    wl = W.qwen3_14b_multispan(gpu, layers=2, history=2048, dst_fill="random")
+    src_o = oracle_side(wl.src, wl.src_mode, wl.src_index)
+    dst_o = oracle_side(wl.dst, wl.dst_mode, wl.dst_index)
+    orc.shift_spans(oracle_spans(wl.spans), src_o, dst_o, wl.inv_freq.numpy(), "bf16")
+    before = [bits(t) for t in wl.dst.caches[0]]
+    plan = wl.plan(direct=False, order="none")
+    torch.cuda.synchronize(gpu)
+    (d,) = plan.descs
+    n = int(d.total_tokens)
+    L = _lib.lib()
+    stream = ctypes.c_void_p(current_stream(gpu))
+    for name, order in (("reversed", np.arange(n - 1, -1, -1)),
+                        ("one entry out of range", np.r_[np.arange(n - 1), n + 5])):
+        for t, b in zip(wl.dst.caches[0], before):
+            t.copy_(torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(gpu))
+        order_dev = torch.from_numpy(order.astype(np.int32)).to(gpu)
+        flags = torch.zeros(1, dtype=torch.int32, device=gpu)
+        d.token_order = order_dev.data_ptr()
+        d.error_flags = flags.data_ptr()
+        _lib.check(L.mkv_shift_spans(ctypes.byref(d), stream))
+        torch.cuda.synchronize(gpu)
+        if name == "reversed":
+            assert int(flags.item()) == 0
+            for layer, t in enumerate(wl.dst.caches[0]):
+                assert np.array_equal(bits(t), dst_o.caches[0][layer]), f"{name} layer {layer}"
+        else:
+            assert int(flags.item()) & _lib.MKV_FLAG_SPAN
+            for layer, t in enumerate(wl.dst.caches[0]):
+                got = bits(t).transpose(0, 2, 1, 3)  # one row per (block, offset)
+                ok = (got == before[layer].transpose(0, 2, 1, 3)).all(axis=(-1, -2)) | (
+                    got == dst_o.caches[0][layer].transpose(0, 2, 1, 3)).all(axis=(-1, -2))
+                assert bool(ok.all()), f"{name} layer {layer}"
+                # the last token (never named) was not moved: its row kept its old bytes
+                last = int(wl.dst_index[-1])
+                assert np.array_equal(bits(t)[last // 16, :, last % 16],
+                                      before[layer][last // 16, :, last % 16])
+    d.token_order = None

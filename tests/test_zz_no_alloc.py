@@ -68,7 +68,7 @@ def _run_case(gpu, wl, order="none"):
         assert np.array_equal(a, want.caches[0][layer]), f"layer {layer}: differs from the oracle"
 
 
-@pytest.mark.parametrize("order", ["none", "dst_page"])
+@pytest.mark.parametrize("order", ["none", "dst_page", "dst_page_device"])
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
 def test_noalloc_matches_the_workspace_entry_point_twice(gpu, dtype, order):
     for layers, history in ((3, 6144), (2, 1024)):  # the second call is smaller
