@@ -101,7 +101,7 @@
 #endif
 // Layers one workgroup moves (grid.y = ceil(layers / this)), each pass's token metadata
 // resolved once for all of them.  The direct path moves MKV_DIRECT_WIDE_LAYERS layers per
-// workgroup when a shift of 2- or 4-byte elements has more than MKV_DIRECT_WIDE_MIN_ROWS
+// workgroup when a shift of 2-byte elements has more than MKV_DIRECT_WIDE_MIN_ROWS
 // (token, layer) rows, and one layer otherwise; the record path MKV_LAYERS_RECORDS.
 #ifndef MKV_DIRECT_WIDE_LAYERS
 #define MKV_DIRECT_WIDE_LAYERS 4
@@ -1480,7 +1480,7 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
 }
 
 // direct_layers: the direct path's layers per workgroup (1, or MKV_DIRECT_WIDE_LAYERS for
-// a larger shift of 2-byte or 4-byte elements); 0 = the record path.
+// a larger shift of 2-byte elements); 0 = the record path.
 template <bool BATCHED>
 int launch_any(int dtype, bool uniform, int direct_layers, const ShiftParams& sp,
                int64_t tiles, int layers, hipStream_t stream) {
@@ -1489,7 +1489,7 @@ int launch_any(int dtype, bool uniform, int direct_layers, const ShiftParams& sp
   case DT:                                                                                  \
     if constexpr (BATCHED) {                                                                \
       if (uniform && direct_layers > 0) {                                                   \
-        if constexpr (DT != MKV_FP8_E4M3 && MKV_DIRECT_WIDE_LAYERS > 1) {                   \
+        if constexpr (Elem<DT>::kBytes == 2 && MKV_DIRECT_WIDE_LAYERS > 1) {                \
           if (direct_layers > 1)                                                            \
             return launch_shift<DT, true, true, true, MKV_DIRECT_WIDE_LAYERS>(sp, tiles,    \
                                                                               layers, stream); \
@@ -1720,8 +1720,10 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
     sp.starts = d->span_starts;
     sp.n_spans = d->n_spans;
     sp.tables = d->span_tables;
+    // several layers per workgroup only for 2-byte elements: fp8 would hold 16 rows' data
+    // across its two passes per wave, fp32 its four passes' (255 VGPRs, 2 waves per SIMD)
     const int direct_layers =
-        d->dtype != MKV_FP8_E4M3 && d->total_tokens * d->layers > MKV_DIRECT_WIDE_MIN_ROWS
+        eb == 2 && d->total_tokens * d->layers > MKV_DIRECT_WIDE_MIN_ROWS
             ? MKV_DIRECT_WIDE_LAYERS
             : 1;
     return launch_any<true>(d->dtype, true, direct_layers, sp, tiles, d->layers, st);
