@@ -112,6 +112,16 @@
 #ifndef MKV_LAYERS_RECORDS
 #define MKV_LAYERS_RECORDS 1
 #endif
+// The same for the record path's per-lane form (heads not a multiple of a wave's rows:
+// one GPU's share of the KV heads under tensor parallelism), for 1-byte elements and
+// for the others.  fp8 at 4 / 2 / 1 heads: two layers 3.0 / 3.0 / 1.7% faster than one
+// (a token's record then serves twice the bytes); bf16 at 2 / 1 heads 1.6 / 2.4% slower.
+#ifndef MKV_LAYERS_RECORDS_NU_1B
+#define MKV_LAYERS_RECORDS_NU_1B 2
+#endif
+#ifndef MKV_LAYERS_RECORDS_NU
+#define MKV_LAYERS_RECORDS_NU MKV_LAYERS_RECORDS
+#endif
 // 1: the batched kernels fetch group 0's base addresses for their layers before the
 // token metadata (the usual single-session shift then needs no dependent fetch of
 // them).  Direct path, record path.
@@ -123,23 +133,20 @@
 #endif
 // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs; with
 // the remap, XCD k walks the k-th contiguous eighth of the tiles (smaller per-XCD set
-// of pages in flight).  0 = plain order.
+// of pages in flight).  1 = plain order everywhere.
 #ifndef MKV_XCDS
 #define MKV_XCDS 8
 #endif
-// The same for 1-byte elements (fp8), whose kernels take their own value: 1, plain order.
-// With the plan's tokens sorted by destination page (the host order), dealing consecutive
-// tiles to all XCDs at once measured 3.9% faster on the fp8 Qwen3-14B shift and 0.3-2.4%
-// on its tensor-parallel shares (1.2% slower with identity block tables); for 2-byte
-// elements the XCD-aware order stays faster (32 sessions: 3.4%).
-#ifndef MKV_XCDS_1B
-#define MKV_XCDS_1B 1
+// Shifts whose token rows (K and V of every head of a token, one layer) span fewer
+// bytes than this take the plain order: with the plan's tokens sorted by destination
+// page, dealing consecutive tiles to all XCDs at once measured faster for them (fp8 at
+// 8 heads, 2 KB a token: 3.8%; bf16 at 4 / 2 / 1 heads: 4.8 / 3.6 / 2.7%), while 4 KB
+// tokens (bf16 at 8 heads, 64 KB paged blocks) keep the XCD-aware order (headline 0.6%,
+// 32 sessions 3.4% faster with it).
+#ifndef MKV_XCD_MIN_TOKEN_BYTES
+#define MKV_XCD_MIN_TOKEN_BYTES 4096
 #endif
-// Grids are padded to a multiple of this (the largest XCD count of any element type).
-#define MKV_GRID_PAD (MKV_XCDS > MKV_XCDS_1B ? MKV_XCDS : MKV_XCDS_1B)
-static_assert(MKV_XCDS >= 1 && MKV_XCDS_1B >= 1 && MKV_GRID_PAD % MKV_XCDS == 0 &&
-                  MKV_GRID_PAD % MKV_XCDS_1B == 0,
-              "the XCD counts must divide the grid padding");
+static_assert(MKV_XCDS >= 1, "MKV_XCDS");
 // Which rows a wave's passes take when it makes more than one (fp8, fp32): 0 = pass u of
 // wave w takes the tile's row group w + waves * u (the waves interleave); 1 = w * passes + u
 // (a wave's passes take adjacent row groups: for 8 heads, adjacent tokens).
@@ -153,9 +160,11 @@ constexpr int kThreads = MKV_WG_THREADS;  // shift kernel; a multiple of the 64-
 constexpr int kWaves = kThreads / 64;
 
 // layers per workgroup of the record path (the direct path picks its own per launch)
-template <bool BATCHED>
+template <int DT, bool BATCHED, bool UNIFORM>
 constexpr int layer_batch() {
-  return BATCHED ? MKV_LAYERS_RECORDS : 1;
+  return !BATCHED   ? 1
+         : UNIFORM ? MKV_LAYERS_RECORDS
+                   : (DT == MKV_FP8_E4M3 ? MKV_LAYERS_RECORDS_NU_1B : MKV_LAYERS_RECORDS_NU);
 }
 constexpr int kPlanThreads = 256;  // plan kernel
 // Buffer resources for the stores: raw (stride 0), the whole 32-bit range checked by
@@ -285,6 +294,8 @@ struct ShiftParams {
   uint32_t heads_magic;  // ceil(2^32 / heads): r / heads == umulhi(r, magic), r < 2^16
   int32_t rotate;        // single span: tables present
   int32_t n_spans;       // direct
+  int32_t xcds;          // MKV_XCDS: XCD-aware tile order; 1: plain order
+  int32_t pad2;
 };
 
 // A small shift's tables, carried in the launch's kernel arguments (no device copy):
@@ -878,12 +889,11 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   const int layer0 = blockIdx.y * LB;
 
   int64_t tile = blockIdx.x;
-  constexpr int kXcds = E::kBytes == 1 ? MKV_XCDS_1B : MKV_XCDS;
-  if constexpr (kXcds > 1) {
-    // gridDim.x is a multiple of MKV_GRID_PAD, which kXcds divides; the map is a
+  if (p.xcds > 1) {
+    // gridDim.x is a multiple of MKV_XCDS (p.xcds is MKV_XCDS or 1); the map is a
     // bijection on [0, gridDim.x)
-    const int64_t per = gridDim.x / kXcds;
-    tile = (blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+    const int64_t per = gridDim.x / MKV_XCDS;
+    tile = (blockIdx.x % MKV_XCDS) * per + blockIdx.x / MKV_XCDS;
   }
   const int64_t g0 = tile * p.tile_tokens;
   if constexpr (DIRECT && !SMALL) {
@@ -1437,6 +1447,7 @@ struct Geometry {
   int tile_tokens;
   bool uniform;
   uint32_t heads_magic;
+  int xcds;  // the tile order (MKV_XCD_MIN_TOKEN_BYTES)
 };
 
 int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_hs,
@@ -1468,6 +1479,8 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_
   g.heads_magic =
       heads == 1 ? 0u : static_cast<uint32_t>(((uint64_t{1} << 32) + heads - 1) / heads);
   g.uniform = heads % g.rows_per_wave == 0;
+  g.xcds = static_cast<int64_t>(heads) * 2 * head_size * eb >= MKV_XCD_MIN_TOKEN_BYTES ? MKV_XCDS
+                                                                                       : 1;
   // per-lane address parts are 32-bit
   const int64_t hs_max = src_hs > dst_hs ? src_hs : dst_hs;
   const int64_t lane_max =
@@ -1479,9 +1492,9 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_
 
 template <int DT, bool BATCHED, bool UNIFORM, bool DIRECT, int LB>
 int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t stream) {
-  // tiles is rounded up to a multiple of MKV_GRID_PAD below; extra workgroups exit at once
+  // tiles is rounded up to a multiple of MKV_XCDS below; extra workgroups exit at once
   if (tiles <= 0) return MKV_OK;
-  tiles = (tiles + MKV_GRID_PAD - 1) / MKV_GRID_PAD * MKV_GRID_PAD;
+  tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
   const int layer_groups = (layers + LB - 1) / LB;
   if (tiles > 0x7FFFFFFF || layer_groups > 65535)
     return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
@@ -1499,7 +1512,7 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
 template <bool BATCHED>
 int launch_any(int dtype, bool uniform, int direct_layers, const ShiftParams& sp,
                int64_t tiles, int layers, hipStream_t stream) {
-  constexpr int RL = layer_batch<BATCHED>();
+
 #define MKV_CASE(DT)                                                                        \
   case DT:                                                                                  \
     if constexpr (BATCHED) {                                                                \
@@ -1512,8 +1525,11 @@ int launch_any(int dtype, bool uniform, int direct_layers, const ShiftParams& sp
         return launch_shift<DT, true, true, true, 1>(sp, tiles, layers, stream);            \
       }                                                                                     \
     }                                                                                       \
-    return uniform ? launch_shift<DT, BATCHED, true, false, RL>(sp, tiles, layers, stream)  \
-                   : launch_shift<DT, BATCHED, false, false, RL>(sp, tiles, layers, stream);
+    return uniform                                                                          \
+               ? launch_shift<DT, BATCHED, true, false, layer_batch<DT, BATCHED, true>()>(     \
+                     sp, tiles, layers, stream)                                             \
+               : launch_shift<DT, BATCHED, false, false, layer_batch<DT, BATCHED, false>()>(   \
+                     sp, tiles, layers, stream);
   switch (dtype) {
     MKV_CASE(MKV_BF16)
     MKV_CASE(MKV_F16)
@@ -1662,6 +1678,7 @@ extern "C" int mkv_scatter_shifted(const void* src, int64_t src_token_stride,
   sp.heads = heads;
   sp.rotary = rot ? rotary : 0;
   sp.tile_tokens = g.tile_tokens;
+  sp.xcds = g.xcds;
   sp.chunks_per_row = g.chunks_per_row;
   sp.rows_per_wave = g.rows_per_wave;
   sp.heads_magic = g.heads_magic;
@@ -1716,6 +1733,7 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   sp.heads = d->heads;
   sp.rotary = d->rotary;
   sp.tile_tokens = g.tile_tokens;
+  sp.xcds = g.xcds;
   sp.chunks_per_row = g.chunks_per_row;
   sp.rows_per_wave = g.rows_per_wave;
   sp.heads_magic = g.heads_magic;
@@ -1835,7 +1853,7 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
 
 template <int DT>
 int launch_small(const SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
-  tiles = (tiles + MKV_GRID_PAD - 1) / MKV_GRID_PAD * MKV_GRID_PAD;
+  tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
   // LDS for the rotation tables of the spans one workgroup may touch
   const size_t lds = static_cast<size_t>(a.p.n_spans) * 2 * a.p.rotary * sizeof(float);
   hipLaunchKernelGGL(shift_small_kernel<DT>,
@@ -1934,6 +1952,7 @@ extern "C" int mkv_shift_spans_small(const mkv_shift_desc_t* d, void* stream) {
   sp.heads = d->heads;
   sp.rotary = d->rotary;
   sp.tile_tokens = g.tile_tokens;
+  sp.xcds = g.xcds;
   sp.chunks_per_row = g.chunks_per_row;
   sp.rows_per_wave = g.rows_per_wave;
   sp.heads_magic = g.heads_magic;
