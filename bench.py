@@ -733,6 +733,8 @@ def _ceiling_lib():
     lib.ceil_stream_copy.argtypes = [vp, vp, i64, i32, vp]
     lib.ceil_paged_copy.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64, i32,
                                     i32, i64, i64, i64, i64, i64, i64, vp]
+    lib.ceil_paged_copy_lanes.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
+                                          i32, i32, i64, i64, i64, i64, i64, i64, i32, vp]
     return lib
 
 
@@ -765,6 +767,9 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
       (``shuffled``) or identity tables (``identity``), with no rotation and no token
       metadata beyond the two block ids: bf16 from the store's K/V planes (64 KB blocks),
       fp8 from its fused rows (32 KB blocks), as the headline and its fp8 twin read them.
+    * ``paged_copy_*_1head_shuffled_*``: the same copy of one GPU's share under tensor
+      parallelism 8 (1 KV head), each lane finding its own (token, head) row as the
+      shift kernel's per-lane path does, with ``sc1 nt`` buffer or ``nt`` global stores.
 
     Every copy is checked after timing: the stream copy whole, the paged copy on sampled
     rows."""
@@ -801,55 +806,83 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
     del a, b
     torch.cuda.empty_cache()
 
-    n = 22141
     rng = np.random.default_rng(0)
     for dname, make in (("bf16", W.qwen3_14b_multispan), ("fp8", W.qwen3_14b_multispan_fp8)):
         wl = make(dev)
-        eb = wl.dst.first.element_size()
-        heads, d, layers = wl.dst.heads, wl.dst.head_size, wl.layers
-        s_k, s_v, _, s_ready, _ = wl.src.device_tables(dev)
-        d_k, d_v, _, d_ready, _ = wl.dst.device_tables(dev)
-        torch.cuda.synchronize()
-        s_str = [x * eb for x in wl.src.strides]
-        d_str = [x * eb for x in wl.dst.strides]
-        src_blocks, dst_blocks = wl.src.first.shape[0], wl.dst.first.shape[0]
-        need = -(-n // 16)
         tables = {
             "shuffled": (np.asarray(wl.meta["src_table"], np.int32),
                          np.asarray(wl.meta["dst_table"], np.int32)),
-            "identity": (np.arange(src_blocks, dtype=np.int32),
-                         np.arange(dst_blocks, dtype=np.int32)),
+            "identity": (np.arange(wl.src.first.shape[0], dtype=np.int32),
+                         np.arange(wl.dst.first.shape[0], dtype=np.int32)),
         }
         for tname, (st_np, dt_np) in tables.items():
-            st_dev = torch.from_numpy(st_np).to(dev)
-            dt_dev = torch.from_numpy(dt_np).to(dev)
-
-            def launch(st_dev=st_dev, dt_dev=dt_dev):
-                rc = lib.ceil_paged_copy(s_k, s_v, d_k, d_v, layers, st_dev.data_ptr(),
-                                         st_dev.numel(), src_blocks, dt_dev.data_ptr(),
-                                         dt_dev.numel(), dst_blocks, n, heads, d * eb,
-                                         *s_str, *d_str, st)
-                if rc != 0:
-                    raise RuntimeError(f"ceil_paged_copy returned {rc}")
-
-            ms = _time_launch(launch, runs, stream)
-            for _ in range(32):  # sampled rows: the destination row is the source row
-                pos, layer = int(rng.integers(n)), int(rng.integers(layers))
-                sb, db, off = int(st_np[pos // 16]), int(dt_np[pos // 16]), pos % 16
-                want = wl.src.fused(0, layer, (sb, off))  # [heads, 2D]
-                got = wl.dst.caches[0][layer][db, :, off]
-                if not torch.equal(want.contiguous().view(torch.uint8),
-                                   got.contiguous().view(torch.uint8)):
-                    raise AssertionError(f"paged_copy_{dname}_{tname}: row {pos} layer {layer}")
-            moved = 2 * n * layers * heads * 2 * d * eb
-            gbs = moved / (ms / 1e3) / 1e9
-            out[f"paged_copy_{dname}_{tname}"] = {
-                "bytes": moved, "ms": round(ms, 4), "GB_s": round(gbs, 1),
-                "frac_of_peak": round(gbs / PEAK_GBS, 4), "blocks_kb": 16 * heads * 2 * d * eb // 1024}
-            assert need <= len(st_np) and need <= len(dt_np)
+            out[f"paged_copy_{dname}_{tname}"] = _paged_copy(
+                lib, wl, st_np, dt_np, None, runs, stream, rng, f"paged_copy_{dname}_{tname}")
+        del wl
+        torch.cuda.empty_cache()
+    # one GPU's share under tensor parallelism 8 (1 KV head): rows of 256 B (bf16) or
+    # 128 B (fp8), a wave's rows spanning tokens, each lane resolving its own row
+    for dname, make in (("bf16", W.qwen3_14b_multispan), ("fp8", W.qwen3_14b_multispan_fp8)):
+        wl = make(dev, heads=1)
+        st_np = np.asarray(wl.meta["src_table"], np.int32)
+        dt_np = np.asarray(wl.meta["dst_table"], np.int32)
+        for sname, scope in (("sc1_nt", 1), ("nt", 0)):
+            name = f"paged_copy_{dname}_1head_shuffled_{sname}"
+            out[name] = _paged_copy(lib, wl, st_np, dt_np, scope, runs, stream, rng, name)
         del wl
         torch.cuda.empty_cache()
     return out
+
+
+def _paged_copy(lib, wl, st_np, dt_np, lanes_scope, runs: int, stream, rng, name: str) -> dict:
+    """Time one paged copy of the workload's 22,141 tokens x every layer from its store
+    blocks into its paged cache through the given block tables, and check 32 sampled
+    rows.  ``lanes_scope`` None: ``ceil_paged_copy`` (a wave's rows in one token);
+    0 or 1: ``ceil_paged_copy_lanes`` with ``nt`` or ``sc1 nt`` stores."""
+    import ctypes
+
+    import torch
+
+    dev = wl.dst.first.device
+    n = 22141
+    st = ctypes.c_void_p(stream.cuda_stream)
+    eb = wl.dst.first.element_size()
+    heads, d, layers = wl.dst.heads, wl.dst.head_size, wl.layers
+    s_k, s_v, _, _, _ = wl.src.device_tables(dev)
+    d_k, d_v, _, _, _ = wl.dst.device_tables(dev)
+    torch.cuda.synchronize()
+    s_str = [x * eb for x in wl.src.strides]
+    d_str = [x * eb for x in wl.dst.strides]
+    src_blocks, dst_blocks = wl.src.first.shape[0], wl.dst.first.shape[0]
+    need = -(-n // 16)
+    assert need <= len(st_np) and need <= len(dt_np)
+    st_dev = torch.from_numpy(st_np).to(dev)
+    dt_dev = torch.from_numpy(dt_np).to(dev)
+    args = (s_k, s_v, d_k, d_v, layers, st_dev.data_ptr(), st_dev.numel(), src_blocks,
+            dt_dev.data_ptr(), dt_dev.numel(), dst_blocks, n, heads, d * eb, *s_str, *d_str)
+
+    def launch():
+        if lanes_scope is None:
+            rc = lib.ceil_paged_copy(*args, st)
+        else:
+            rc = lib.ceil_paged_copy_lanes(*args, lanes_scope, st)
+        if rc != 0:
+            raise RuntimeError(f"{name}: the copy kernel returned {rc}")
+
+    ms = _time_launch(launch, runs, stream)
+    for _ in range(32):  # sampled rows: the destination row is the source row
+        pos, layer = int(rng.integers(n)), int(rng.integers(layers))
+        sb, db, off = int(st_np[pos // 16]), int(dt_np[pos // 16]), pos % 16
+        want = wl.src.fused(0, layer, (sb, off))  # [heads, 2D]
+        got = wl.dst.caches[0][layer][db, :, off]
+        if not torch.equal(want.contiguous().view(torch.uint8),
+                           got.contiguous().view(torch.uint8)):
+            raise AssertionError(f"{name}: row {pos} layer {layer}")
+    moved = 2 * n * layers * heads * 2 * d * eb
+    gbs = moved / (ms / 1e3) / 1e9
+    return {"bytes": moved, "ms": round(ms, 4), "GB_s": round(gbs, 1),
+            "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "blocks_kb": 16 * heads * 2 * d * eb / 1024}
 
 
 def dst_layouts(dev, steps: int, warmup: int, stream) -> dict:

@@ -12,6 +12,10 @@
 //    access pattern (a token's K and V rows of every head, 16 bytes per lane, lane j of a
 //    row owning chunk j of K and chunk j of V) with nothing resolved but the two block
 //    ids, and no arithmetic on the data.
+//  * ceil_paged_copy_lanes: the same copy with each lane finding its own (token, head)
+//    row, so a wave's rows may span tokens (one GPU's 1, 2 or 4 KV heads under tensor
+//    parallelism); block ids are per-lane loads and the stores go through the layer's
+//    buffer resource (sc1 nt) or plain non-temporal global stores.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -106,6 +110,40 @@ __global__ __launch_bounds__(128) void paged_copy_kernel(PagedCopy p) {
   store_at<18>(dv, d_lane, v);
 }
 
+// 128 threads: two waves of rows_per_wave rows each, rows (token, head) in token order;
+// a lane's token and head come from its own row number.  Destination byte offsets within
+// a layer stay below 2^31 (checked on the host), so a layer's base is the store's
+// wave-uniform resource and the lane's offset its 32-bit voffset.
+template <int CPOL>
+__global__ __launch_bounds__(128) void paged_copy_lane_kernel(PagedCopy p) {
+  const int64_t tile = xcd_tile();
+  const int layer = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row_in_wave = lane / p.chunks;
+  const int j = lane - row_in_wave * p.chunks;
+  if (row_in_wave >= p.rows_per_wave) return;
+  // rows (n_tokens * heads, padded to whole tiles) stay below 2^31: 32-bit division
+  const uint32_t row = static_cast<uint32_t>((tile * 2 + wave) * p.rows_per_wave + row_in_wave);
+  const uint32_t pos = row / static_cast<uint32_t>(p.heads);
+  const int64_t h = row - pos * static_cast<uint32_t>(p.heads);
+  if (pos >= p.n_tokens) return;
+  const int64_t sb = p.src_table[pos >> 4];
+  const int64_t db = p.dst_table[pos >> 4];
+  if (sb < 0 || sb >= p.src_blocks || db < 0 || db >= p.dst_blocks) return;
+  const int64_t off = pos & 15;
+  const int64_t s_at = sb * p.s_block + off * p.s_off + h * p.s_head + j * 16;
+  const uint32_t d_at = static_cast<uint32_t>(db * p.d_block + off * p.d_off + h * p.d_head + j * 16);
+  const char* sk = reinterpret_cast<const char*>(ld_const(p.src_k + layer));
+  const char* sv = reinterpret_cast<const char*>(ld_const(p.src_v + layer));
+  char* dk = reinterpret_cast<char*>(ld_const(p.dst_k + layer));
+  char* dv = reinterpret_cast<char*>(ld_const(p.dst_v + layer));
+  const u32x4 k = load_nt(sk + s_at);
+  const u32x4 v = load_nt(sv + s_at);
+  store_at<CPOL>(dk, d_at, k);
+  store_at<CPOL>(dv, d_at, v);
+}
+
 int grid_x(int64_t tiles, unsigned* out) {
   tiles = (tiles + kXcds - 1) / kXcds * kXcds;
   if (tiles <= 0 || tiles > 0x7FFFFFFF) return 1;
@@ -136,31 +174,24 @@ extern "C" int ceil_stream_copy(const void* src, void* dst, int64_t bytes, int32
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// Positions [0, n_tokens) of every layer, block size 16.  Tables hold at least
-// ceil(n_tokens / 16) entries (src_table_len, dst_table_len); block ids outside
-// [0, *_blocks) skip their rows.  row_bytes: bytes of K (and of V) per (token, head),
-// a multiple of 16 of at most 1 KB; heads a multiple of 64 / (row_bytes / 16).  Strides
-// in bytes, multiples of 16, lane offsets within 2^31.
-extern "C" int ceil_paged_copy(const uint64_t* src_k, const uint64_t* src_v, const uint64_t* dst_k,
-                               const uint64_t* dst_v, int32_t layers, const int32_t* src_table,
-                               int64_t src_table_len, int64_t src_blocks,
-                               const int32_t* dst_table, int64_t dst_table_len,
-                               int64_t dst_blocks, int64_t n_tokens, int32_t heads,
-                               int32_t row_bytes, int64_t s_block, int64_t s_head, int64_t s_off,
-                               int64_t d_block, int64_t d_head, int64_t d_off, void* stream) {
+namespace {
+
+// The two paged copies' shared argument checks; fills p (tile_tokens unset).
+int paged_args(PagedCopy& p, const uint64_t* src_k, const uint64_t* src_v, const uint64_t* dst_k,
+               const uint64_t* dst_v, int32_t layers, const int32_t* src_table,
+               int64_t src_table_len, int64_t src_blocks, const int32_t* dst_table,
+               int64_t dst_table_len, int64_t dst_blocks, int64_t n_tokens, int32_t heads,
+               int32_t row_bytes, int64_t s_block, int64_t s_head, int64_t s_off, int64_t d_block,
+               int64_t d_head, int64_t d_off) {
   if (!src_k || !src_v || !dst_k || !dst_v || !src_table || !dst_table) return 1;
   if (layers <= 0 || layers > 65535 || n_tokens <= 0 || heads <= 0) return 1;
+  if (src_blocks <= 0 || dst_blocks <= 0) return 1;
   if (row_bytes <= 0 || row_bytes % 16 != 0 || row_bytes > 1024) return 1;
-  const int chunks = row_bytes / 16;
-  const int rpw = 64 / chunks;
-  if (heads % rpw != 0) return 1;
   const int64_t need = (n_tokens + 15) / 16;
   if (src_table_len < need || dst_table_len < need) return 1;
   const int64_t strides[6] = {s_block, s_head, s_off, d_block, d_head, d_off};
   for (int64_t s : strides)
     if (s < 0 || s % 16 != 0) return 1;
-  if ((rpw - 1) * (s_head > d_head ? s_head : d_head) + row_bytes >= (int64_t{1} << 31)) return 1;
-  PagedCopy p;
   p.src_k = src_k;
   p.src_v = src_v;
   p.dst_k = dst_k;
@@ -177,8 +208,33 @@ extern "C" int ceil_paged_copy(const uint64_t* src_k, const uint64_t* src_v, con
   p.d_head = d_head;
   p.d_off = d_off;
   p.heads = heads;
-  p.chunks = chunks;
-  p.rows_per_wave = rpw;
+  p.chunks = row_bytes / 16;
+  p.rows_per_wave = 64 / p.chunks;
+  return 0;
+}
+
+}  // namespace
+
+// Positions [0, n_tokens) of every layer, block size 16.  Tables hold at least
+// ceil(n_tokens / 16) entries (src_table_len, dst_table_len); block ids outside
+// [0, *_blocks) skip their rows.  row_bytes: bytes of K (and of V) per (token, head),
+// a multiple of 16 of at most 1 KB; heads a multiple of 64 / (row_bytes / 16).  Strides
+// in bytes, multiples of 16, lane offsets within 2^31.
+extern "C" int ceil_paged_copy(const uint64_t* src_k, const uint64_t* src_v, const uint64_t* dst_k,
+                               const uint64_t* dst_v, int32_t layers, const int32_t* src_table,
+                               int64_t src_table_len, int64_t src_blocks,
+                               const int32_t* dst_table, int64_t dst_table_len,
+                               int64_t dst_blocks, int64_t n_tokens, int32_t heads,
+                               int32_t row_bytes, int64_t s_block, int64_t s_head, int64_t s_off,
+                               int64_t d_block, int64_t d_head, int64_t d_off, void* stream) {
+  PagedCopy p;
+  if (paged_args(p, src_k, src_v, dst_k, dst_v, layers, src_table, src_table_len, src_blocks,
+                 dst_table, dst_table_len, dst_blocks, n_tokens, heads, row_bytes, s_block, s_head,
+                 s_off, d_block, d_head, d_off) != 0)
+    return 1;
+  const int rpw = p.rows_per_wave;
+  if (heads % rpw != 0) return 1;
+  if ((rpw - 1) * (s_head > d_head ? s_head : d_head) + row_bytes >= (int64_t{1} << 31)) return 1;
   const int rows = 2 * rpw;  // two waves
   p.tile_tokens = rows / heads > 0 ? rows / heads : 1;
   if (p.tile_tokens * heads != rows) return 1;  // a tile is whole tokens
@@ -186,5 +242,42 @@ extern "C" int ceil_paged_copy(const uint64_t* src_k, const uint64_t* src_v, con
   if (grid_x((n_tokens + p.tile_tokens - 1) / p.tile_tokens, &gx) != 0) return 1;
   hipLaunchKernelGGL(paged_copy_kernel, dim3(gx, static_cast<unsigned>(layers)), dim3(128), 0,
                      static_cast<hipStream_t>(stream), p);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// As ceil_paged_copy for any number of heads, each lane resolving its own row.  The
+// destination's last byte of a layer ((dst_blocks - 1) * d_block + 15 * d_off +
+// (heads - 1) * d_head + row_bytes) must stay below 2^31.  device_scope: 1 = sc1 nt
+// buffer stores, 0 = non-temporal global stores.
+extern "C" int ceil_paged_copy_lanes(const uint64_t* src_k, const uint64_t* src_v,
+                                     const uint64_t* dst_k, const uint64_t* dst_v, int32_t layers,
+                                     const int32_t* src_table, int64_t src_table_len,
+                                     int64_t src_blocks, const int32_t* dst_table,
+                                     int64_t dst_table_len, int64_t dst_blocks, int64_t n_tokens,
+                                     int32_t heads, int32_t row_bytes, int64_t s_block,
+                                     int64_t s_head, int64_t s_off, int64_t d_block, int64_t d_head,
+                                     int64_t d_off, int32_t device_scope, void* stream) {
+  PagedCopy p;
+  if (paged_args(p, src_k, src_v, dst_k, dst_v, layers, src_table, src_table_len, src_blocks,
+                 dst_table, dst_table_len, dst_blocks, n_tokens, heads, row_bytes, s_block, s_head,
+                 s_off, d_block, d_head, d_off) != 0)
+    return 1;
+  const int64_t limit = int64_t{1} << 31;
+  if (dst_blocks > limit || d_block > limit || d_off > limit || d_head > limit) return 1;
+  const int64_t last = (dst_blocks - 1) * d_block + 15 * d_off + (heads - 1) * d_head + row_bytes;
+  if (last >= limit) return 1;
+  const int64_t rows = n_tokens * heads;
+  const int64_t per_tile = 2 * p.rows_per_wave;
+  if (rows > limit - per_tile * kXcds) return 1;
+  p.tile_tokens = 0;  // unused: rows, not tokens, make the tiles
+  unsigned gx = 0;
+  if (grid_x((rows + per_tile - 1) / per_tile, &gx) != 0) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (device_scope)
+    hipLaunchKernelGGL(paged_copy_lane_kernel<18>, dim3(gx, static_cast<unsigned>(layers)),
+                       dim3(128), 0, st, p);
+  else
+    hipLaunchKernelGGL(paged_copy_lane_kernel<-1>, dim3(gx, static_cast<unsigned>(layers)),
+                       dim3(128), 0, st, p);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }

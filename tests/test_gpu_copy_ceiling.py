@@ -1,7 +1,8 @@
 """The benchmark's ceiling copies (tests/hip/copy_ceiling.hip) copy exactly what they claim
 to: the stream copy byte for byte with either store policy, and the paged copy every row
 of positions [0, n) through both block tables -- bf16 from K/V planes, fp8 from fused
-rows, into an HND cache -- leaving every other row untouched."""
+rows, into an HND cache -- leaving every other row untouched, with a wave's rows in one
+token (8 heads) or each lane resolving its own row (1, 2 or 8 heads, either store)."""
 
 from __future__ import annotations
 
@@ -25,6 +26,8 @@ def _lib():
     lib.ceil_stream_copy.argtypes = [vp, vp, i64, i32, vp]
     lib.ceil_paged_copy.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64, i32,
                                     i32, i64, i64, i64, i64, i64, i64, vp]
+    lib.ceil_paged_copy_lanes.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
+                                          i32, i32, i64, i64, i64, i64, i64, i64, i32, vp]
     return lib
 
 
@@ -42,12 +45,18 @@ def test_stream_copy(gpu, scope, nbytes):
     assert lib.ceil_stream_copy(src.data_ptr(), dst.data_ptr(), 24, scope, None) == 1
 
 
+# (heads, lanes): lanes None = ceil_paged_copy, 0 / 1 = ceil_paged_copy_lanes with nt /
+# sc1 nt stores
+CASES = [(8, None), (8, 0), (8, 1), (2, 1), (1, 0), (1, 1)]
+
+
+@pytest.mark.parametrize("heads,lanes", CASES)
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])
-def test_paged_copy(gpu, dtype):
-    print(f"case paged copy {dtype}", flush=True)
+def test_paged_copy(gpu, dtype, heads, lanes):
+    print(f"case paged copy {dtype} heads={heads} lanes={lanes}", flush=True)
     lib = _lib()
     make = W.qwen3_14b_multispan if dtype == "bf16" else W.qwen3_14b_multispan_fp8
-    wl = make(gpu, layers=3, history=1024)
+    wl = make(gpu, layers=3, history=1024, heads=heads)
     eb = wl.dst.first.element_size()
     heads, d = wl.dst.heads, wl.dst.head_size
     src_blocks, dst_blocks = wl.src.first.shape[0], wl.dst.first.shape[0]
@@ -60,10 +69,13 @@ def test_paged_copy(gpu, dtype):
     d_k, d_v, _, _, _ = wl.dst.device_tables(gpu)
     torch.cuda.synchronize(gpu)
     st_dev, dt_dev = torch.from_numpy(st).to(gpu), torch.from_numpy(dt).to(gpu)
-    rc = lib.ceil_paged_copy(s_k, s_v, d_k, d_v, wl.layers, st_dev.data_ptr(), st.size,
-                             src_blocks, dt_dev.data_ptr(), dt.size, dst_blocks, n, heads, d * eb,
-                             *[x * eb for x in wl.src.strides], *[x * eb for x in wl.dst.strides],
-                             None)
+    args = (s_k, s_v, d_k, d_v, wl.layers, st_dev.data_ptr(), st.size, src_blocks,
+            dt_dev.data_ptr(), dt.size, dst_blocks, n, heads, d * eb,
+            *[x * eb for x in wl.src.strides], *[x * eb for x in wl.dst.strides])
+    if lanes is None:
+        rc = lib.ceil_paged_copy(*args, None)
+    else:
+        rc = lib.ceil_paged_copy_lanes(*args, lanes, None)
     assert rc == 0
     torch.cuda.synchronize(gpu)
     pos = np.arange(n)
@@ -75,7 +87,8 @@ def test_paged_copy(gpu, dtype):
         got = wl.dst.caches[0][layer]
         assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), f"layer {layer}"
     # tables shorter than the positions need are refused
-    assert lib.ceil_paged_copy(s_k, s_v, d_k, d_v, wl.layers, st_dev.data_ptr(), 2, src_blocks,
-                               dt_dev.data_ptr(), dt.size, dst_blocks, n, heads, d * eb,
-                               *[x * eb for x in wl.src.strides],
-                               *[x * eb for x in wl.dst.strides], None) == 1
+    short = (*args[:6], 2, *args[7:])
+    if lanes is None:
+        assert lib.ceil_paged_copy(*short, None) == 1
+    else:
+        assert lib.ceil_paged_copy_lanes(*short, lanes, None) == 1
