@@ -73,6 +73,10 @@
 #ifndef MKV_PASSES_1B
 #define MKV_PASSES_1B 2
 #endif
+// fp8's passes per wave in the per-lane form (heads not a multiple of a wave's rows).
+#ifndef MKV_PASSES_1B_NU
+#define MKV_PASSES_1B_NU MKV_PASSES_1B
+#endif
 
 // 1: store V before rotating K (frees its registers during the rotation).  Measured
 // 11% slower for bf16: a row's K and V halves are adjacent, and writing them far apart
@@ -212,10 +216,16 @@ struct Elem<MKV_FP8_E4M3> {
   static constexpr int kBytes = 1, kPerChunk = 16, kPasses = MKV_PASSES_1B;
 };
 
-int passes_of(int dt) {
+// Wave passes per workgroup: the element type's, or fp8's per-lane count.
+template <int DT, bool UNIFORM>
+constexpr int passes() {
+  return DT == MKV_FP8_E4M3 && !UNIFORM ? MKV_PASSES_1B_NU : Elem<DT>::kPasses;
+}
+
+int passes_of(int dt, bool uniform) {
   switch (dt) {
     case MKV_FP8_E4M3:
-      return MKV_PASSES_1B;
+      return uniform ? MKV_PASSES_1B : MKV_PASSES_1B_NU;
     case MKV_F32:
       return MKV_PASSES_4B;
     default:
@@ -881,7 +891,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   static_assert(!SMALL || DIRECT, "small shifts take the direct path");
   using E = Elem<DT>;
   constexpr int C = E::kPerChunk;
-  constexpr int U = E::kPasses;
+  constexpr int U = passes<DT, UNIFORM>();
   static_assert(LB >= 1 && (BATCHED || LB == 1), "one layer per single-span launch");
   constexpr int N = U * LB;  // (pass, layer) units of one sweep: x = u * LB + lb
 
@@ -1499,14 +1509,14 @@ int check_geometry(int dtype, int heads, int head_size, int rotary, int64_t src_
   if (g.chunks_per_row > 64)
     return fail(MKV_ERR_UNSUPPORTED, "row of %d chunks exceeds one wave", g.chunks_per_row);
   g.rows_per_wave = 64 / g.chunks_per_row;
-  const int rows = g.rows_per_wave * kWaves * passes_of(dtype);
+  g.uniform = heads % g.rows_per_wave == 0;
+  const int rows = g.rows_per_wave * kWaves * passes_of(dtype, g.uniform);
   g.tile_tokens = rows / heads > 0 ? rows / heads : 1;
   // row -> (token, head) uses a 32-bit reciprocal, exact while rows < 2^16
   if (static_cast<int64_t>(g.tile_tokens) * heads >= (1 << 16))
     return fail(MKV_ERR_UNSUPPORTED, "heads %d too large", heads);
   g.heads_magic =
       heads == 1 ? 0u : static_cast<uint32_t>(((uint64_t{1} << 32) + heads - 1) / heads);
-  g.uniform = heads % g.rows_per_wave == 0;
   g.xcds = static_cast<int64_t>(heads) * 2 * head_size * eb >= MKV_XCD_MIN_TOKEN_BYTES ? MKV_XCDS
                                                                                        : 1;
   // per-lane address parts are 32-bit
