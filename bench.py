@@ -767,6 +767,8 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
       (``shuffled``) or identity tables (``identity``), with no rotation and no token
       metadata beyond the two block ids: bf16 from the store's K/V planes (64 KB blocks),
       fp8 from its fused rows (32 KB blocks), as the headline and its fp8 twin read them.
+    * ``paged_copy_*_runs_of_G_blocks``: the same copy with both block tables shuffled in
+      runs of G consecutive blocks, up to one 2 MB translation page per run.
     * ``paged_copy_*_1head_shuffled_*``: the same copy of one GPU's share under tensor
       parallelism 8 (1 KV head), each lane finding its own (token, head) row as the
       shift kernel's per-lane path does, with ``sc1 nt`` buffer or ``nt`` global stores.
@@ -818,6 +820,17 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
         for tname, (st_np, dt_np) in tables.items():
             out[f"paged_copy_{dname}_{tname}"] = _paged_copy(
                 lib, wl, st_np, dt_np, None, runs, stream, rng, f"paged_copy_{dname}_{tname}")
+        # both tables permuted in runs of G consecutive blocks (G = 1: every block on its
+        # own; the largest G makes a run one 2 MB translation page): how the cost of
+        # scattered blocks fades as the runs grow
+        blk_bytes = 16 * wl.dst.heads * 2 * wl.dst.head_size * wl.dst.first.element_size()
+        page_blocks = (2 << 20) // blk_bytes
+        perm = np.random.default_rng(7)
+        for g in (1, 4, page_blocks):
+            st_np = _run_permutation(wl.src.first.shape[0], g, perm)
+            dt_np = _run_permutation(wl.dst.first.shape[0], g, perm)
+            name = f"paged_copy_{dname}_runs_of_{g}_blocks"
+            out[name] = _paged_copy(lib, wl, st_np, dt_np, None, runs, stream, rng, name)
         del wl
         torch.cuda.empty_cache()
     # one GPU's share under tensor parallelism 8 (1 KV head): rows of 256 B (bf16) or
@@ -832,6 +845,15 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
         del wl
         torch.cuda.empty_cache()
     return out
+
+
+def _run_permutation(n: int, run: int, rng):
+    """A block table over n blocks that keeps runs of ``run`` consecutive blocks together
+    and shuffles the runs (the last run may be short)."""
+    import numpy as np
+
+    starts = np.arange(0, n, run)[rng.permutation(-(-n // run))]
+    return np.concatenate([np.arange(a, min(a + run, n)) for a in starts]).astype(np.int32)
 
 
 def _paged_copy(lib, wl, st_np, dt_np, lanes_scope, runs: int, stream, rng, name: str) -> dict:
