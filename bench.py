@@ -1075,11 +1075,12 @@ def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
                         lambda: W.qwen3_14b_multispan_fp8(dev, heads=1))):
         log(f"record order A/B: {name}")
         wl = make()
-        t0 = time.perf_counter()
-        wl.plan(direct=False, order="none")
-        t1 = time.perf_counter()
-        wl.plan(direct=False, order="dst_page")
-        t2 = time.perf_counter()
+        build_ms = {}
+        for order in ("none", "dst_page") * 3:  # the first builds carry one-time costs
+            t0 = time.perf_counter()
+            wl.plan(direct=False, order=order)
+            ms_ = (time.perf_counter() - t0) * 1e3
+            build_ms[order] = min(build_ms.get(order, ms_), ms_)
         plans = {"none": wl.plan(direct=False, order="none"),
                  "dst_page": wl.plan(direct=False, order="dst_page"),
                  "dst_addr": wl.plan(direct=False, order="dst_addr"),
@@ -1097,7 +1098,7 @@ def plan_variants(dev, steps: int, warmup: int, stream) -> dict:
             "dst_page_gain_pct": round(100 * (ms["none"] / ms["dst_page"] - 1), 2),
             "dst_addr_gain_pct": round(100 * (ms["none"] / ms["dst_addr"] - 1), 2),
             "dst_page_device_gain_pct": round(100 * (ms["none"] / ms["dst_page_device"] - 1), 2),
-            "host_order_ms": round((t2 - t1 - (t1 - t0)) * 1e3, 3),
+            "host_order_ms": round(build_ms["dst_page"] - build_ms["none"], 3),
             "bit_identical": same,
         }
         del wl, plans
