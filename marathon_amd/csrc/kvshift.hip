@@ -318,7 +318,7 @@ struct ShiftParams {
   int32_t rotate;        // single span: tables present
   int32_t n_spans;       // direct
   int32_t xcds;          // MKV_XCDS: XCD-aware tile order; 1: plain order
-  int32_t pad2;
+  int32_t xcd_per;       // set at launch: gridDim.x / MKV_XCDS with xcds > 1, else 0
 };
 
 // A small shift's tables, carried in the launch's kernel arguments (no device copy):
@@ -911,12 +911,26 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   const int H = p.heads;
   const int layer0 = blockIdx.y * LB;
 
+  // The fields the first metadata and data fetches need are loaded in the kernel's first
+  // batch of scalar loads, with those the tile decisions below read, rather than in a
+  // second dependent batch behind the early exits (the compiler does not hoist loads
+  // above them on its own): one kernel-argument round trip fewer ahead of the data.
+  if constexpr (!BATCHED) {
+    asm volatile("" ::"s"(p.s_k), "s"(p.s_v), "s"(p.d_k), "s"(p.d_v), "s"(p.src_tstride));
+  } else if constexpr (!DIRECT) {
+    asm volatile("" ::"s"(p.recs), "s"(p.src_k_base), "s"(p.src_v_base), "s"(p.dst_k_base),
+                 "s"(p.dst_v_base), "s"(p.tables), "s"(p.k_scale), "s"(p.src_hstride),
+                 "s"(p.dst_hstride));
+  } else if constexpr (!SMALL) {
+    asm volatile("" ::"s"(p.starts), "s"(p.spans), "s"(p.n_spans));
+  }
   int64_t tile = blockIdx.x;
-  if (p.xcds > 1) {
-    // gridDim.x is a multiple of MKV_XCDS (p.xcds is MKV_XCDS or 1); the map is a
-    // bijection on [0, gridDim.x)
-    const int64_t per = gridDim.x / MKV_XCDS;
-    tile = (blockIdx.x % MKV_XCDS) * per + blockIdx.x / MKV_XCDS;
+  if (p.xcd_per > 0) {
+    // gridDim.x == MKV_XCDS * xcd_per (the launch pads the grid): a bijection on
+    // [0, gridDim.x).  The launch passes xcd_per rather than the kernel reading
+    // gridDim.x, whose hidden argument would be one more dependent scalar load ahead
+    // of the first data load.
+    tile = static_cast<int64_t>(blockIdx.x % MKV_XCDS) * p.xcd_per + blockIdx.x / MKV_XCDS;
   }
   const int64_t g0 = tile * p.tile_tokens;
   if constexpr (DIRECT && !SMALL) {
@@ -1537,9 +1551,11 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
   if (tiles > 0x7FFFFFFF || layer_groups > 65535)
     return fail(MKV_ERR_UNSUPPORTED, "grid of %lld x %d tiles too large", (long long)tiles,
                 layer_groups);
+  ShiftParams q = sp;
+  q.xcd_per = sp.xcds > 1 ? static_cast<int32_t>(tiles / MKV_XCDS) : 0;
   hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT, LB>),
                      dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layer_groups)),
-                     dim3(kThreads), 0, stream, sp);
+                     dim3(kThreads), 0, stream, q);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
   return MKV_OK;
@@ -1890,8 +1906,10 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
 }
 
 template <int DT>
-int launch_small(const SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
+int launch_small(SmallParams& a, int64_t tiles, int layers, hipStream_t stream) {
   tiles = (tiles + MKV_XCDS - 1) / MKV_XCDS * MKV_XCDS;
+  if (tiles > 0x7FFFFFFF) return fail(MKV_ERR_UNSUPPORTED, "grid of %lld tiles too large", (long long)tiles);
+  a.p.xcd_per = a.p.xcds > 1 ? static_cast<int32_t>(tiles / MKV_XCDS) : 0;
   // LDS for the rotation tables of the spans one workgroup may touch
   const size_t lds = static_cast<size_t>(a.p.n_spans) * 2 * a.p.rotary * sizeof(float);
   hipLaunchKernelGGL(shift_small_kernel<DT>,
