@@ -731,6 +731,7 @@ def _ceiling_lib():
     lib = ctypes.CDLL(CEILING_LIB)
     i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
     lib.ceil_stream_copy.argtypes = [vp, vp, i64, i32, vp]
+    lib.ceil_stream_copy_persistent.argtypes = [vp, vp, i64, i32, vp]
     lib.ceil_paged_copy.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64, i32,
                                     i32, i64, i64, i64, i64, i64, i64, vp]
     lib.ceil_paged_copy_lanes.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
@@ -761,7 +762,8 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
     * ``stream_copy_*``: one contiguous 3.63 GB buffer into another (the headline's
       7.26 GB read once and written once), 16 bytes per thread, one-shot grid, XCD-aware
       order, non-temporal loads; stores non-temporal (``nt``) or device-scope streaming
-      (``sc1 nt``, the shift kernel's stores).
+      (``sc1 nt``, the shift kernel's stores).  ``*_persistent_*``: the same copy by a
+      fixed grid of 1,024 / 2,048 / 8,192 workgroups walking the buffer.
     * ``paged_copy_*``: the headline's 22,141 tokens x 40 layers from the session store's
       blocks into the HND paged cache, through the headline's own shuffled block tables
       (``shuffled``) or identity tables (``identity``), with no rotation and no token
@@ -805,6 +807,21 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
         gbs = 2 * nbytes / (ms / 1e3) / 1e9
         out[name] = {"bytes": 2 * nbytes, "ms": round(ms, 4), "GB_s": round(gbs, 1),
                      "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    # the same copy by a persistent grid (workgroups walking the buffer in grid strides)
+    for wgs in (1024, 2048, 8192):
+        name = f"stream_copy_sc1_nt_persistent_{wgs}_workgroups"
+        b.zero_()
+
+        def launch(wgs=wgs):
+            if lib.ceil_stream_copy_persistent(a.data_ptr(), b.data_ptr(), nbytes, wgs, st) != 0:
+                raise RuntimeError("ceil_stream_copy_persistent refused its arguments")
+
+        ms = _time_launch(launch, runs, stream)
+        if not torch.equal(a, b):
+            raise AssertionError(f"{name}: the copy differs from its source")
+        gbs = 2 * nbytes / (ms / 1e3) / 1e9
+        out[name] = {"bytes": 2 * nbytes, "ms": round(ms, 4), "GB_s": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_GBS, 4), "workgroups": wgs}
     del a, b
     torch.cuda.empty_cache()
 

@@ -7,6 +7,9 @@
 //    contiguous range, non-temporal loads, and stores either non-temporal (global) or
 //    device-scope streaming (sc1 nt, through a buffer resource whose base is the
 //    workgroup's first byte).
+//  * ceil_stream_copy_persistent: the same copy with a fixed grid whose workgroups walk
+//    the buffer in grid-sized strides (a persistent kernel), for comparison with the
+//    one-shot grid.
 //  * ceil_paged_copy: token positions [0, n) of a paged source into positions [0, n) of
 //    a paged destination, both through 16-token block tables, every layer: the shift's
 //    access pattern (a token's K and V rows of every head, 16 bytes per lane, lane j of a
@@ -62,6 +65,17 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const char* src, char*
   if (i >= n16) return;
   const u32x4 v = load_nt(src + i * 16);
   store_at<CPOL>(dst + tile * 4096, threadIdx.x * 16u, v);
+}
+
+// Persistent: workgroup b copies 4 KB tiles b, b + gridDim.x, ... (256 threads, one
+// 16-byte vector each per tile).
+template <int CPOL>
+__global__ __launch_bounds__(256) void stream_copy_persistent_kernel(const char* src, char* dst,
+                                                                      int64_t n16, int64_t tiles) {
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t i = tile * 256 + threadIdx.x;
+    if (i < n16) store_at<CPOL>(dst + tile * 4096, threadIdx.x * 16u, load_nt(src + i * 16));
+  }
 }
 
 struct PagedCopy {
@@ -214,6 +228,22 @@ int paged_args(PagedCopy& p, const uint64_t* src_k, const uint64_t* src_v, const
 }
 
 }  // namespace
+
+// As ceil_stream_copy (sc1 nt stores) with a fixed grid of `workgroups` workgroups
+// (1..65535) walking the buffer.  Returns 0, 1 on a bad argument, 2 on a failed launch.
+extern "C" int ceil_stream_copy_persistent(const void* src, void* dst, int64_t bytes,
+                                           int32_t workgroups, void* stream) {
+  if (src == nullptr || dst == nullptr || bytes <= 0 || bytes % 16 != 0 || workgroups <= 0 ||
+      workgroups > 65535 ||
+      (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0)
+    return 1;
+  const int64_t n16 = bytes / 16;
+  const int64_t tiles = (n16 + 255) / 256;
+  hipLaunchKernelGGL(stream_copy_persistent_kernel<18>, dim3(static_cast<unsigned>(workgroups)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const char*>(src), static_cast<char*>(dst), n16, tiles);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 // Positions [0, n_tokens) of every layer, block size 16.  Tables hold at least
 // ceil(n_tokens / 16) entries (src_table_len, dst_table_len); block ids outside

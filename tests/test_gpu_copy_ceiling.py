@@ -1,5 +1,6 @@
 """The benchmark's ceiling copies (tests/hip/copy_ceiling.hip) copy exactly what they claim
-to: the stream copy byte for byte with either store policy, and the paged copy every row
+to: the stream copy byte for byte with either store policy and by a persistent grid,
+and the paged copy every row
 of positions [0, n) through both block tables -- bf16 from K/V planes, fp8 from fused
 rows, into an HND cache -- leaving every other row untouched, with a wave's rows in one
 token (8 heads) or each lane resolving its own row (1, 2 or 8 heads, either store)."""
@@ -24,6 +25,7 @@ def _lib():
     lib = ctypes.CDLL(LIB)
     i32, i64, vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
     lib.ceil_stream_copy.argtypes = [vp, vp, i64, i32, vp]
+    lib.ceil_stream_copy_persistent.argtypes = [vp, vp, i64, i32, vp]
     lib.ceil_paged_copy.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64, i32,
                                     i32, i64, i64, i64, i64, i64, i64, vp]
     lib.ceil_paged_copy_lanes.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
@@ -43,6 +45,20 @@ def test_stream_copy(gpu, scope, nbytes):
     assert torch.equal(dst[:nbytes], src[:nbytes])
     assert int(dst[nbytes:].count_nonzero()) == 0  # nothing past the end
     assert lib.ceil_stream_copy(src.data_ptr(), dst.data_ptr(), 24, scope, None) == 1
+
+
+@pytest.mark.parametrize("wgs", [1, 7, 300])
+@pytest.mark.parametrize("nbytes", [16, 4096 * 8 + 48, 3 * 2**20 + 16])
+def test_stream_copy_persistent(gpu, wgs, nbytes):
+    print(f"case persistent stream copy workgroups={wgs} bytes={nbytes}", flush=True)
+    lib = _lib()
+    src = torch.randint(0, 255, (nbytes + 64,), dtype=torch.uint8, device=gpu)
+    dst = torch.zeros_like(src)
+    assert lib.ceil_stream_copy_persistent(src.data_ptr(), dst.data_ptr(), nbytes, wgs, None) == 0
+    torch.cuda.synchronize(gpu)
+    assert torch.equal(dst[:nbytes], src[:nbytes])
+    assert int(dst[nbytes:].count_nonzero()) == 0
+    assert lib.ceil_stream_copy_persistent(src.data_ptr(), dst.data_ptr(), nbytes, 0, None) == 1
 
 
 # (heads, lanes): lanes None = ceil_paged_copy, 0 / 1 = ceil_paged_copy_lanes with nt /
