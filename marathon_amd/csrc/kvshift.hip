@@ -164,6 +164,22 @@
 #define MKV_XCD_MIN_TOKEN_BYTES 4096
 #endif
 static_assert(MKV_XCDS >= 1, "MKV_XCDS");
+// Record-path shifts reading from at least MKV_LAYER_MAJOR_MIN_GROUPS source groups
+// (sessions' stores) and moving at least MKV_LAYER_MAJOR_MIN_TOKENS tokens take a
+// one-dimensional grid with the layer groups fastest: a tile's layers run back to back
+// on one XCD, so the workgroups running together hold a few tokens' rows of every layer
+// rather than many tokens of one layer, from few sessions' stores rather than from all
+// of them.  Measured in one process against the two-dimensional grid (layers slowest):
+// 32 sessions (250K tokens) 2.8-5.2% faster and 16 sessions (116K) 2.5-4.2% (the
+// translation misses of the vector caches fall by 39% at 32 sessions); 1, 2, 4 or 8
+// sessions, or 16 and 32 short ones, within +-1.5% or slower (up to 12% for the fp8
+// single-session shift).
+#ifndef MKV_LAYER_MAJOR_MIN_GROUPS
+#define MKV_LAYER_MAJOR_MIN_GROUPS 16
+#endif
+#ifndef MKV_LAYER_MAJOR_MIN_TOKENS
+#define MKV_LAYER_MAJOR_MIN_TOKENS 100000
+#endif
 // Which rows a wave's passes take when it makes more than one (fp8, fp32): 0 = pass u of
 // wave w takes the tile's row group w + waves * u (the waves interleave); 1 = w * passes + u
 // (a wave's passes take adjacent row groups: for 8 heads, adjacent tokens).
@@ -318,7 +334,10 @@ struct ShiftParams {
   int32_t rotate;        // single span: tables present
   int32_t n_spans;       // direct
   int32_t xcds;          // MKV_XCDS: XCD-aware tile order; 1: plain order
-  int32_t xcd_per;       // set at launch: gridDim.x / MKV_XCDS with xcds > 1, else 0
+  int32_t xcd_per;       // set at launch: tiles per XCD with xcds > 1, else 0
+  int32_t layer_groups;  // the layer-major grid: 1 = asked for (host), then the layer
+                         // groups at launch; 0: two-dimensional
+  int32_t pad3;
 };
 
 // A small shift's tables, carried in the launch's kernel arguments (no device copy):
@@ -909,7 +928,6 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   const int partner_addr = (partner & 63) * 4;
   const uint32_t chunk_off = static_cast<uint32_t>(j) * 16u;
   const int H = p.heads;
-  const int layer0 = blockIdx.y * LB;
 
   // The fields the first metadata and data fetches need are loaded in the kernel's first
   // batch of scalar loads, with those the tile decisions below read, rather than in a
@@ -925,13 +943,28 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     asm volatile("" ::"s"(p.starts), "s"(p.spans), "s"(p.n_spans));
   }
   int64_t tile = blockIdx.x;
-  if (p.xcd_per > 0) {
+  int lgroup = blockIdx.y;
+  if (BATCHED && !DIRECT && p.layer_groups > 0) {
+    // gridDim.x == tiles * layer_groups: XCD k takes tiles [k * xcd_per, (k + 1) *
+    // xcd_per), each tile's layer groups in turn; plain order: tile-major, layers fastest
+    const int64_t b = blockIdx.x;
+    const int LG = p.layer_groups;
+    if (p.xcd_per > 0) {
+      const int64_t local = b / MKV_XCDS;
+      lgroup = static_cast<int>(local % LG);
+      tile = (b % MKV_XCDS) * p.xcd_per + local / LG;
+    } else {
+      lgroup = static_cast<int>(b % LG);
+      tile = b / LG;
+    }
+  } else if (p.xcd_per > 0) {
     // gridDim.x == MKV_XCDS * xcd_per (the launch pads the grid): a bijection on
     // [0, gridDim.x).  The launch passes xcd_per rather than the kernel reading
     // gridDim.x, whose hidden argument would be one more dependent scalar load ahead
     // of the first data load.
     tile = static_cast<int64_t>(blockIdx.x % MKV_XCDS) * p.xcd_per + blockIdx.x / MKV_XCDS;
   }
+  const int layer0 = lgroup * LB;
   const int64_t g0 = tile * p.tile_tokens;
   if constexpr (DIRECT && !SMALL) {
     // one workgroup checks the caller's prefix against the span table: starts[0] == 0,
@@ -1553,9 +1586,14 @@ int launch_shift(const ShiftParams& sp, int64_t tiles, int layers, hipStream_t s
                 layer_groups);
   ShiftParams q = sp;
   q.xcd_per = sp.xcds > 1 ? static_cast<int32_t>(tiles / MKV_XCDS) : 0;
-  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT, LB>),
-                     dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(layer_groups)),
-                     dim3(kThreads), 0, stream, q);
+  q.layer_groups = 0;
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(layer_groups));
+  if (BATCHED && !DIRECT && sp.layer_groups != 0 && tiles * layer_groups <= 0x7FFFFFFF) {
+    q.layer_groups = layer_groups;
+    grid = dim3(static_cast<unsigned>(tiles * layer_groups), 1);
+  }
+  hipLaunchKernelGGL((shift_kernel<DT, BATCHED, UNIFORM, DIRECT, LB>), grid, dim3(kThreads), 0,
+                     stream, q);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "launch failed: %s", hipGetErrorString(e));
   return MKV_OK;
@@ -1902,6 +1940,8 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   sp.tables = tables;
   sp.src_hstride = src_hs;
   sp.dst_hstride = dst_hs;
+  sp.layer_groups = d->src.groups >= MKV_LAYER_MAJOR_MIN_GROUPS &&
+                    d->total_tokens >= MKV_LAYER_MAJOR_MIN_TOKENS;
   return launch_any<true>(d->dtype, g.uniform, 0, sp, tiles, d->layers, st);
 }
 

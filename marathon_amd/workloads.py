@@ -331,9 +331,10 @@ def batched_sessions_layouts(seed: int = 5, sessions: int = 32, hist_lo: int = 2
 
 
 def batched_sessions(device, layers: int = 36, seed: int = 5, sessions: int = 32, hist_lo: int = 2048,
-            hist_hi: int = 32768, dtype=torch.bfloat16) -> Workload:
+            hist_hi: int = 32768, dtype=torch.bfloat16, heads: int = HEADS) -> Workload:
     """32 sessions, each its own store (group), one shared HND destination pool; both
-    sides addressed through block tables, so the slot math runs on the device."""
+    sides addressed through block tables, so the slot math runs on the device.  fp8:
+    per-layer K and V scales shared by the sessions."""
     lays = batched_sessions_layouts(seed, sessions, hist_lo, hist_hi)
     rng = np.random.default_rng(seed + 1000)
     gen = torch.Generator(device=device)
@@ -341,20 +342,27 @@ def batched_sessions(device, layers: int = 36, seed: int = 5, sessions: int = 32
     dst_need = [-(-lay.dst_history // BLOCK) for lay in lays]
     pool = int(sum(dst_need)) + 64
     perm = rng.permutation(pool).astype(np.int32)
+    fp8 = dtype == torch.float8_e4m3fn
+    k_scale = v_scale = None
+    if fp8:
+        k, v = fp8_layer_scales(seed, layers)
+        k_scale, v_scale = torch.from_numpy(k), torch.from_numpy(v)
     src_tables, dst_tables, src_caches, rows = [], [], [], []
     s_off = d_off = 0
     for g, lay in enumerate(lays):
         nb = -(-lay.src_history // BLOCK)
         src_tables.append(rng.permutation(nb).astype(np.int32))
         dst_tables.append(perm[d_off : d_off + dst_need[g]])
-        src_caches.append([store_blocks(nb, HEADS, dtype, gen, device,
+        src_caches.append([store_blocks(nb, heads, dtype, gen, device,
+                                        k_scale[layer] if fp8 else None,
+                                        v_scale[layer] if fp8 else None,
                                         layout=store_layout(dtype))
-                           for _ in range(layers)])
+                           for layer in range(layers)])
         for s, d, n, dl in zip(lay.src_start, lay.dst_start, lay.length, lay.delta):
             rows.append((int(s), int(d), s_off, d_off, int(n), int(dl), g, 0))
         s_off += nb
         d_off += dst_need[g]
-    dst_caches = [torch.zeros(_paged(pool, "hnd"), dtype=dtype, device=device)
+    dst_caches = [torch.zeros(_paged(pool, "hnd", heads), dtype=dtype, device=device)
                   for _ in range(layers)]
     return Workload(
         "batched restore",
@@ -366,6 +374,8 @@ def batched_sessions(device, layers: int = 36, seed: int = 5, sessions: int = 32
         "table",
         torch.from_numpy(np.concatenate(dst_tables)),
         inv_freq_for(HEAD_SIZE, THETA),
+        k_scale,
+        v_scale,
         meta={"layouts": lays, "src_tables": src_tables, "dst_tables": dst_tables},
     )
 

@@ -153,6 +153,22 @@ def test_batched_sessions_full_size(gpu):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("dtype,heads,layers", [("bf16", 8, 3), ("fp8", 1, 5), ("bf16", 2, 3),
+                                                ("fp8", 8, 2)])
+def test_layer_major_grid_every_row(gpu, dtype, heads, layers):
+    """Shifts of 100,000 tokens or more from 16 sessions' stores or more run on the
+    layer-major grid (each tile's layer groups back to back): every row of every layer
+    against the oracle, in the uniform and per-lane forms, with an odd layer count under
+    fp8's two-layer per-lane groups."""
+    print(f"case layer-major grid {dtype} heads={heads} layers={layers}", flush=True)
+    wl = W.batched_sessions(gpu, layers=layers, sessions=16, heads=heads,
+                            dtype=torch.float8_e4m3fn if dtype == "fp8" else torch.bfloat16)
+    assert wl.tokens >= 100_000 and wl.src.groups == 16
+    _check_full(wl, dtype, snapshot=False, direct=False)
+    del wl
+    torch.cuda.empty_cache()
+
+
 def test_round_trip_at_full_size(gpu):
     """Shift by delta, then back by -delta: K returns within the double-rounding bound,
     V exactly."""
