@@ -26,6 +26,8 @@ Prints one JSON line.  Also measured, in the same line:
   rows of its published table.
 * ``tp_shares``: the headline shift at 4, 2 and 1 KV heads (one GPU's share at TP 2, 4,
   8), bf16 and fp8.
+* ``session_batches``: the batched-sessions shift with 16 sessions, in fp8, and at one
+  KV head (bf16 and fp8).
 * ``size_sweep``: one batched shift of 512 to 32,768 tokens x 40 layers, to show where
   the fixed cost of a call stops mattering.
 * ``ceilings``: a plain elementwise copy of the same bytes, and the headline with its
@@ -558,6 +560,38 @@ def other_workloads(dev, steps: int, warmup: int, stream) -> dict:
             "GB_s": round(plan.algorithmic_bytes / (ms / 1e3) / 1e9, 1),
             "frac_of_peak": round(plan.algorithmic_bytes / (ms / 1e3) / 1e9 / PEAK_GBS, 4),
         }
+        del wl, plan
+        torch.cuda.empty_cache()
+    return out
+
+
+def session_batches(dev, steps: int, warmup: int, stream) -> dict:
+    """Informational: the batched-sessions shift (config 5's layout: each session its
+    own store, one shared HND destination pool, 36 layers) in its other forms: 16
+    sessions, fp8 e4m3, and one GPU's share under tensor parallelism 8 (1 KV head) in
+    bf16 and fp8.  One launch per step each."""
+    import numpy as np
+    import torch
+
+    from marathon_amd import workloads as W
+
+    out = {}
+    for name, make in (
+            ("sessions_16_bf16", lambda: W.batched_sessions(dev, sessions=16)),
+            ("sessions_32_fp8", lambda: W.batched_sessions(dev, dtype=torch.float8_e4m3fn)),
+            ("sessions_32_tp8_bf16", lambda: W.batched_sessions(dev, heads=1)),
+            ("sessions_32_tp8_fp8",
+             lambda: W.batched_sessions(dev, heads=1, dtype=torch.float8_e4m3fn))):
+        log(f"timing {name}")
+        wl = make()
+        plan = wl.plan()
+        warm_up(lambda: plan.launch(stream.cuda_stream))
+        _, per = time_plan(plan, steps, warmup, stream)
+        ms = float(np.median(per))
+        gbs = plan.algorithmic_bytes / (ms / 1e3) / 1e9
+        out[name] = {"sessions": int(wl.src.groups), "heads": int(wl.dst.heads),
+                     "tokens": wl.tokens, "layers": wl.layers, "ms": round(ms, 4),
+                     "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
         del wl, plan
         torch.cuda.empty_cache()
     return out
@@ -1389,6 +1423,9 @@ def main() -> int:
                     "multi-span and batched-session workloads")
     ap.add_argument("--no-tp-shares", action="store_true",
                     help="skip the timings of one GPU's share at 4, 2 and 1 KV heads")
+    ap.add_argument("--no-session-batches", action="store_true",
+                    help="skip the batched-sessions shift's other forms (16 sessions, fp8, "
+                    "one KV head)")
     ap.add_argument("--no-size-sweep", action="store_true",
                     help="skip the batched shifts of 512 to 32,768 tokens")
     ap.add_argument("--no-ceilings", action="store_true",
@@ -1413,7 +1450,7 @@ def main() -> int:
     if args.only:
         keep = {x.strip() for x in args.only.split(",") if x.strip()}
         sections = {"reference_shape", "reference_loop", "other_workloads", "tp_shares",
-                    "size_sweep", "ceilings", "dst_layouts", "src_layouts", "src_block_sizes",
+                    "session_batches", "size_sweep", "ceilings", "dst_layouts", "src_layouts", "src_block_sizes",
                     "connector_step", "plan_variants", "cpu_baseline"}
         if keep - sections - {"headline"}:  # "headline": the headline line alone
             ap.error(f"--only: unknown sections {sorted(keep - sections)}")
@@ -1483,6 +1520,9 @@ def main() -> int:
     if not args.no_tp_shares:
         log("tensor-parallel shares of the headline shift (4, 2, 1 KV heads)")
         extra["tp_shares"] = tp_shares(dev, side_steps, args.warmup, stream)
+    if not args.no_session_batches:
+        log("batched sessions: 16 sessions, fp8, one KV head")
+        extra["session_batches"] = session_batches(dev, side_steps, args.warmup, stream)
     if not args.no_size_sweep:
         log("size sweep: one batched shift of 512 to 32,768 tokens x 40 layers")
         extra["size_sweep"] = size_sweep(dev, side_steps, args.warmup, stream)
