@@ -173,7 +173,8 @@ static_assert(MKV_XCDS >= 1, "MKV_XCDS");
 // 32 sessions (250K tokens) 2.8-5.2% faster and 16 sessions (116K) 2.5-4.2% (the
 // translation misses of the vector caches fall by 39% at 32 sessions); 1, 2, 4 or 8
 // sessions, or 16 and 32 short ones, within +-1.5% or slower (up to 12% for the fp8
-// single-session shift).
+// single-session shift); the reverse, saves from one paged pool into 16 or 32 stores,
+// 4.6% slower, so only source groups count.
 #ifndef MKV_LAYER_MAJOR_MIN_GROUPS
 #define MKV_LAYER_MAJOR_MIN_GROUPS 16
 #endif
