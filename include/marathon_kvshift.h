@@ -35,11 +35,10 @@
  * per-layer scale, rotates in fp32 and requantises:
  *     x = fl32(decode(code) * k_scale[layer]);   y = rotation of x as above;
  *     q = e4m3fn_RNE(clamp(fl32(y / k_scale[layer]), -448, 448))   (NaN -> 0x7F)
- * The quotient is evaluated with Markstein's correction (marathon_amd/csrc/fp8_e4m3.h);
- * it equals the correctly rounded fl32(y / k_scale) for every y that can change a code
- * at every scale checked exhaustively (every K scale of this library's fp8 workloads and
- * tests) and on 3e8 random pairs over 41 binades of scale; other scales are covered by
- * that random sample only.
+ * The quotient is evaluated without a division per element (marathon_amd/csrc/fp8_e4m3.h:
+ * the reciprocal split in two, then one Markstein correction); it equals the correctly
+ * rounded fl32(y / k_scale) for every finite y at every k_scale in [2^-90, 2^100], the
+ * range a K scale must lie in.
  * V bytes are copied raw for every element type.
  */
 #ifndef MARATHON_KVSHIFT_H
@@ -148,8 +147,9 @@ typedef struct mkv_side {
  *                  launch and the workspace); tokens beyond it are not moved and raise
  *                  MKV_FLAG_SPAN.
  *   inv_freq     : device fp32 [rotary / 2]; may be NULL when rotary == 0.
- *   k_scale      : device fp32 [layers] for MKV_FP8_E4M3 when rotary > 0; otherwise
- *                  ignored and may be NULL (with rotary 0 every K byte is copied).
+ *   k_scale      : device fp32 [layers] for MKV_FP8_E4M3 when rotary > 0, each in
+ *                  [2^-90, 2^100]; otherwise ignored and may be NULL (with rotary 0 every
+ *                  K byte is copied).
  *   error_flags  : device int32 [1] or NULL.
  *   workspace    : device, >= mkv_shift_workspace_size(total_tokens, n_spans, rotary)
  *                  bytes, 16-byte aligned; overwritten by every call, so calls that
@@ -224,7 +224,7 @@ typedef struct mkv_shift_desc {
  *             rotary/2 <= i < rotary); cos == NULL is a plain scatter (delta 0).
  * rotary    : rotated dimensions (2 * len(inv_freq)); dims >= rotary are copied.
  *             n_tokens == 0 is a no-op.
- * k_scale   : device fp32 [1] for MKV_FP8_E4M3 when rotating, else NULL.
+ * k_scale   : device fp32 [1], in [2^-90, 2^100], for MKV_FP8_E4M3 when rotating, else NULL.
  * Tokens move concurrently, as in the Triton kernel: a slot repeated in `slots` gets
  * one of its tokens, which one is unspecified; `src` must not alias `kv`.
  */

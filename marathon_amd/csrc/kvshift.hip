@@ -470,7 +470,7 @@ struct Rotor;
 template <>
 struct Rotor<MKV_BF16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, const mkv_fp8::Divisor&) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -487,7 +487,7 @@ struct Rotor<MKV_BF16> {
 template <>
 struct Rotor<MKV_F16> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, const mkv_fp8::Divisor&) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -504,7 +504,7 @@ struct Rotor<MKV_F16> {
 template <>
 struct Rotor<MKV_F32> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float, float) {
+                                              const float* s, const mkv_fp8::Divisor&) {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -523,7 +523,7 @@ struct Rotor<MKV_F32> {
 template <>
 struct Rotor<MKV_FP8_E4M3> {
   static __device__ __forceinline__ u32x4 run(u32x4 mine, u32x4 part, const float* c,
-                                              const float* s, float scale, float rcp) {
+                                              const float* s, const mkv_fp8::Divisor& dv) {
     using namespace mkv_fp8;
     u32x4 out;
 #pragma unroll
@@ -534,7 +534,7 @@ struct Rotor<MKV_FP8_E4M3> {
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int e = 4 * w + b;
-        q[b] = quant(rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]), scale, rcp);
+        q[b] = quant(rot1(mk[b] * dv.s, pk[b] * dv.s, c[e], s[e]), dv);
       }
       out[w] = encode4(q);
     }
@@ -550,7 +550,7 @@ struct Rotor<MKV_FP8_E4M3> {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const int e = 4 * w + b;
-          const float y = rot1(mk[b] * scale, pk[b] * scale, c[e], s[e]);
+          const float y = rot1(mk[b] * dv.s, pk[b] * dv.s, c[e], s[e]);
           if (y != y) out[w] = with_nan(out[w], b);
         }
       }
@@ -1015,19 +1015,17 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     lay[lb] = lay_ok[lb] ? layer0 + lb : p.layers - 1;
   }
 
-  float scale[LB], rcp[LB];
+  mkv_fp8::Divisor dv[LB];  // fp8: the layers' K scales
   float cs[C], sg[C];
 #pragma unroll
   for (int e = 0; e < C; ++e) cs[e] = 1.0f, sg[e] = 0.0f;
 #pragma unroll
-  for (int lb = 0; lb < LB; ++lb) scale[lb] = 1.0f;
+  for (int lb = 0; lb < LB; ++lb) dv[lb] = mkv_fp8::unit_divisor();
   int cur_span = -1;
   // a single span's cos/sin and fp8's K scales are loaded behind the first pass's data
   // (phase B), not here: they are needed only for the rotation, and a load in flight at
   // the pass loop's head would hold back the first data loads
   bool scale_ready = DT != MKV_FP8_E4M3;
-#pragma unroll
-  for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f;
 
   // direct (span table in memory): lane k holds span k's fields and prefix entry k,
   // loaded once; a pass finds its span with one ballot and reads the fields from that
@@ -1281,10 +1279,9 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
         // the scale dequantises K for the rotation; with no rotation k_scale may be NULL
         if (BATCHED ? p.rotary > 0 : p.rotate != 0) {
 #pragma unroll
-          for (int lb = 0; lb < LB; ++lb) scale[lb] = ld_const(p.k_scale + (BATCHED ? lay[lb] : 0));
+          for (int lb = 0; lb < LB; ++lb)
+            dv[lb] = mkv_fp8::divisor(ld_const(p.k_scale + (BATCHED ? lay[lb] : 0)));
         }
-#pragma unroll
-        for (int lb = 0; lb < LB; ++lb) rcp[lb] = 1.0f / scale[lb];  // correctly rounded
         scale_ready = true;
       }
     }
@@ -1421,7 +1418,7 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
             cur_span = span_u[u];
           }
         }
-        kd[x] = Rotor<DT>::run(kd[x], pd, cs, sg, scale[lb], rcp[lb]);
+        kd[x] = Rotor<DT>::run(kd[x], pd, cs, sg, dv[lb]);
       }
     }
 

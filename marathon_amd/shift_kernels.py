@@ -193,6 +193,8 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 # fp32 K scales given as Python numbers, kept on their device: the reference's
 # per-layer loop passes the same 40 scales on every load, so each is uploaded once
 _SCALES: dict[tuple[int, int], torch.Tensor] = {}
+# the K scales the fp8 requantisation divides by correctly rounded (include/marathon_kvshift.h)
+_SCALE_MIN, _SCALE_MAX = np.float32(2.0 ** -90), np.float32(2.0 ** 100)
 _SCALES_MAX = 4096
 
 
@@ -203,8 +205,10 @@ def _scale_tensor(k_scale, device) -> torch.Tensor:
             t = t.to(device=device, dtype=torch.float32)
         return t.contiguous()
     value = np.float32(float(k_scale))
+    if not _SCALE_MIN <= value <= _SCALE_MAX:
+        raise ValueError(f"k_scale {float(k_scale)!r} outside [2^-90, 2^100]")
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (int(idx), int(value.view(np.uint32)))  # by bits: -0.0 and NaN stay distinct
+    key = (int(idx), int(value.view(np.uint32)))  # by bits
     t = _SCALES.get(key)
     if t is None:
         if len(_SCALES) >= _SCALES_MAX:

@@ -15,11 +15,11 @@ __global__ void encode_kernel(const float* y, float scale, int quantize, uint32_
                               int64_t n4) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n4) return;
-  const float rcp = 1.0f / scale;
+  const mkv_fp8::Divisor dv = mkv_fp8::divisor(scale);
   float q[4];
   for (int b = 0; b < 4; ++b) {
     const float v = y[4 * i + b];
-    q[b] = quantize ? mkv_fp8::quant(v, scale, rcp) : mkv_fp8::clamp448(v);
+    q[b] = quantize ? mkv_fp8::quant(v, dv) : mkv_fp8::clamp448(v);
   }
   uint32_t w = mkv_fp8::encode4(q);
   for (int b = 0; b < 4; ++b) {

@@ -220,6 +220,16 @@ def test_python_api_refuses_tensors_off_the_gpu():
         scatter_shifted(src, kv, torch.arange(4), 16, True, rope_shift(3, 128, inv, "cpu"))
 
 
+def test_fp8_k_scale_outside_the_exact_division_range_is_refused_on_the_host():
+    """A Python-float K scale must lie where the fp8 quotient is correctly rounded
+    ([2^-90, 2^100]); the check runs before any device tensor is made."""
+    from marathon_amd.shift_kernels import _scale_tensor
+
+    for bad in (0.0, -0.05, float("nan"), float("inf"), 2.0 ** -91, 2.0 ** 101):
+        with pytest.raises(ValueError, match="outside"):
+            _scale_tensor(bad, torch.device("cuda", 0))
+
+
 def test_rope_shift_asserts_rotary_fits():
     inv = torch.ones(80)
     with pytest.raises(AssertionError, match="rotary 160 > head_size 128"):

@@ -1,13 +1,14 @@
 """The fp8 requantisation's division, checked exhaustively on the CPU.
 
-The kernel computes y / k_scale with Markstein's correction (two fmas after a multiply
-by the rounded reciprocal; marathon_amd/csrc/fp8_e4m3.h) and relies on it equalling the
-correctly rounded quotient, which the oracle computes by an IEEE division.  An IEEE
-division in the kernel measured 8% slower on the fp8 Qwen3-14B shift, so the kernel
-keeps Markstein and this test walks, at every K scale the fp8 workloads and the GPU
-tests use, every fp32 y whose quotient can change an e4m3fn code (2^-12 <= |y/s| <
-2^10, both signs: 3.7e8 quotients per scale), plus 3e8 random (scale, y) pairs over 41
-binades of scale.  tests/fp8_division_check.c does the walking.
+The kernel computes y / k_scale without a division per element
+(marathon_amd/csrc/fp8_e4m3.h): q0 = y * rz + RN(y * rlo), from the reciprocal split in
+two, is within one ulp of the quotient, and one Markstein correction with r = RN(1/s)
+then gives the correctly rounded quotient, which the oracle computes by an IEEE
+division.  tests/fp8_division_check.c repeats the kernel's operations and walks, at
+every K scale the fp8 workloads and the GPU tests use and at scales whose reciprocal
+rounds up, down or not at all, every fp32 y whose quotient can change an e4m3fn code
+(2^-12 <= |y/s| < 2^10, both signs: 3.7e8 quotients per scale), plus 3e8 random
+(scale, y) pairs over 41 binades of scale.
 """
 
 from __future__ import annotations
@@ -62,3 +63,20 @@ def test_the_fixed_scales_of_the_fp8_gpu_tests(checker):
 
 def test_random_scales_over_41_binades(checker):
     _run(checker, ["random", "300000000"])
+
+
+def test_scales_by_how_their_reciprocal_rounds(checker):
+    # 0.125: exact reciprocal (rlo = 0); 0.1, 3.0: RN(1/s) above 1/s (rz is its
+    # predecessor); 0.01: below; the largest and smallest significands, where a single
+    # correction from RN(y * r) has the least margin
+    out = _run(checker, _hex([0.125, 0.1, 3.0, 0.01]) + ["3fffffff", "3f800001", "3f7fffff"])
+    assert out.count("scale ") == 7
+
+
+def test_the_walk_finds_a_wrong_quotient(checker):
+    # planted mistake: RN(y * r) with no correction is one ulp off for many y
+    out = subprocess.run([checker, "plain", *_hex([0.1])], capture_output=True, text=True,
+                         timeout=600)
+    assert out.returncode == 1
+    bad = int(out.stdout.strip().rsplit(" ", 2)[-2])
+    assert bad > 1000, out.stdout

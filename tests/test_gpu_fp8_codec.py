@@ -1,7 +1,7 @@
 """The shift kernel's fp8 e4m3fn codec, value by value, on the GPU.
 
-The codec (marathon_amd/csrc/fp8_e4m3.h: gfx950's hardware conversions, the Markstein
-division, the clamp and the NaN rewrite) runs through a small test library
+The codec (marathon_amd/csrc/fp8_e4m3.h: gfx950's hardware conversions, the division
+by the K scale, the clamp and the NaN rewrite) runs through a small test library
 (tests/hip/fp8_codec_probe.hip) on inputs that real shifts reach only by chance:
 every exact midpoint between neighbouring codes (ties to even), the fp32 neighbours of
 each midpoint, the clamp range, signed zeros, subnormals and NaN.  The expected codes
