@@ -770,6 +770,8 @@ def _ceiling_lib():
                                     i32, i64, i64, i64, i64, i64, i64, vp]
     lib.ceil_paged_copy_lanes.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
                                           i32, i32, i64, i64, i64, i64, i64, i64, i32, vp]
+    lib.ceil_paged_copy_ex.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
+                                       i32, i32, i64, i64, i64, i64, i64, i64, i32, vp, vp]
     return lib
 
 
@@ -805,6 +807,10 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
       fp8 from its fused rows (32 KB blocks), as the headline and its fp8 twin read them.
     * ``paged_copy_*_runs_of_G_blocks``: the same copy with both block tables shuffled in
       runs of G consecutive blocks, up to one 2 MB translation page per run.
+    * ``paged_copy_*_kv_split``: the same copy with K and V moved by separate waves (a
+      wave pair per row group); ``*_k_after_read``: each K store held behind one
+      dependent read of a small table after its data arrives, as the shift's rotation
+      holds K behind its cos/sin table.
     * ``paged_copy_*_1head_shuffled_*``: the same copy of one GPU's share under tensor
       parallelism 8 (1 KV head), each lane finding its own (token, head) row as the
       shift kernel's per-lane path does, with ``sc1 nt`` buffer or ``nt`` global stores.
@@ -871,6 +877,13 @@ def copy_ceilings(dev, steps: int, warmup: int, stream) -> dict:
         for tname, (st_np, dt_np) in tables.items():
             out[f"paged_copy_{dname}_{tname}"] = _paged_copy(
                 lib, wl, st_np, dt_np, None, runs, stream, rng, f"paged_copy_{dname}_{tname}")
+            name = f"paged_copy_{dname}_{tname}_kv_split"
+            out[name] = _paged_copy(lib, wl, st_np, dt_np, None, runs, stream, rng, name,
+                                    ex=(1, False))
+        st_np, dt_np = tables["shuffled"]
+        for suffix, ex in (("k_after_read", (0, True)), ("kv_split_k_after_read", (1, True))):
+            name = f"paged_copy_{dname}_shuffled_{suffix}"
+            out[name] = _paged_copy(lib, wl, st_np, dt_np, None, runs, stream, rng, name, ex=ex)
         # both tables permuted in runs of G consecutive blocks (G = 1: every block on its
         # own; the largest G makes a run one 2 MB translation page): how the cost of
         # scattered blocks fades as the runs grow
@@ -907,11 +920,13 @@ def _run_permutation(n: int, run: int, rng):
     return np.concatenate([np.arange(a, min(a + run, n)) for a in starts]).astype(np.int32)
 
 
-def _paged_copy(lib, wl, st_np, dt_np, lanes_scope, runs: int, stream, rng, name: str) -> dict:
+def _paged_copy(lib, wl, st_np, dt_np, lanes_scope, runs: int, stream, rng, name: str,
+                ex=None) -> dict:
     """Time one paged copy of the workload's 22,141 tokens x every layer from its store
     blocks into its paged cache through the given block tables, and check 32 sampled
     rows.  ``lanes_scope`` None: ``ceil_paged_copy`` (a wave's rows in one token);
-    0 or 1: ``ceil_paged_copy_lanes`` with ``nt`` or ``sc1 nt`` stores."""
+    0 or 1: ``ceil_paged_copy_lanes`` with ``nt`` or ``sc1 nt`` stores.  ``ex``
+    (kv_split, k_after_read): ``ceil_paged_copy_ex`` instead."""
     import ctypes
 
     import torch
@@ -934,8 +949,12 @@ def _paged_copy(lib, wl, st_np, dt_np, lanes_scope, runs: int, stream, rng, name
     args = (s_k, s_v, d_k, d_v, layers, st_dev.data_ptr(), st_dev.numel(), src_blocks,
             dt_dev.data_ptr(), dt_dev.numel(), dst_blocks, n, heads, d * eb, *s_str, *d_str)
 
+    zeros = torch.zeros(16, dtype=torch.int32, device=dev)  # the K stores' read table
+
     def launch():
-        if lanes_scope is None:
+        if ex is not None:
+            rc = lib.ceil_paged_copy_ex(*args, ex[0], zeros.data_ptr() if ex[1] else None, st)
+        elif lanes_scope is None:
             rc = lib.ceil_paged_copy(*args, st)
         else:
             rc = lib.ceil_paged_copy_lanes(*args, lanes_scope, st)

@@ -15,6 +15,9 @@
 //    access pattern (a token's K and V rows of every head, 16 bytes per lane, lane j of a
 //    row owning chunk j of K and chunk j of V) with nothing resolved but the two block
 //    ids, and no arithmetic on the data.
+//  * ceil_paged_copy_ex: ceil_paged_copy with K and V optionally moved by separate waves
+//    (a wave pair per row group) and K's store optionally held behind one dependent read
+//    of a small table, as the shift's rotation holds it behind its cos/sin table.
 //  * ceil_paged_copy_lanes: the same copy with each lane finding its own (token, head)
 //    row, so a wave's rows may span tokens (one GPU's 1, 2 or 4 KV heads under tensor
 //    parallelism); block ids are per-lane loads and the stores go through the layer's
@@ -122,6 +125,42 @@ __global__ __launch_bounds__(128) void paged_copy_kernel(PagedCopy p) {
   const u32x4 v = load_nt(sv + s_lane);
   store_at<18>(dk, d_lane, k);
   store_at<18>(dv, d_lane, v);
+}
+
+// ceil_paged_copy's rows, two row groups of rows_per_wave rows per workgroup.  SPLIT: 256
+// threads, wave w moving only K (w even) or only V (w odd) of row group w / 2; else 128
+// threads, each wave moving K and V of its group.  KREAD: K's chunk is stored only after
+// a read of k_read[its first word & 15] (zeros, so the copy stays exact) has returned.
+template <bool SPLIT, bool KREAD>
+__global__ __launch_bounds__(256) void paged_copy_ex_kernel(PagedCopy p, const uint32_t* k_read) {
+  const int64_t tile = xcd_tile();
+  const int layer = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int group = SPLIT ? wave >> 1 : wave;
+  const bool v_only = SPLIT && (wave & 1) != 0;
+  const bool k_only = SPLIT && !v_only;
+  const int row_in_wave = lane / p.chunks;
+  const int j = lane - row_in_wave * p.chunks;
+  const int row0 = group * p.rows_per_wave;
+  const int t = row0 / p.heads;
+  const int h0 = row0 - t * p.heads;
+  const int64_t pos = tile * p.tile_tokens + t;
+  if (pos >= p.n_tokens || row_in_wave >= p.rows_per_wave) return;
+  const int64_t sb = ld_const(p.src_table + (pos >> 4));
+  const int64_t db = ld_const(p.dst_table + (pos >> 4));
+  if (sb < 0 || sb >= p.src_blocks || db < 0 || db >= p.dst_blocks) return;
+  const int64_t off = pos & 15;
+  const int64_t s_row = sb * p.s_block + off * p.s_off + h0 * p.s_head;
+  const int64_t d_row = db * p.d_block + off * p.d_off + h0 * p.d_head;
+  const uint32_t s_lane = static_cast<uint32_t>(row_in_wave * p.s_head) + j * 16u;
+  const uint32_t d_lane = static_cast<uint32_t>(row_in_wave * p.d_head) + j * 16u;
+  u32x4 k{0, 0, 0, 0}, v{0, 0, 0, 0};
+  if (!v_only) k = load_nt(reinterpret_cast<const char*>(ld_const(p.src_k + layer)) + s_row + s_lane);
+  if (!k_only) v = load_nt(reinterpret_cast<const char*>(ld_const(p.src_v + layer)) + s_row + s_lane);
+  if (KREAD && !v_only) k[0] ^= k_read[k[0] & 15u];
+  if (!v_only) store_at<18>(reinterpret_cast<char*>(ld_const(p.dst_k + layer)) + d_row, d_lane, k);
+  if (!k_only) store_at<18>(reinterpret_cast<char*>(ld_const(p.dst_v + layer)) + d_row, d_lane, v);
 }
 
 // 128 threads: two waves of rows_per_wave rows each, rows (token, head) in token order;
@@ -272,6 +311,43 @@ extern "C" int ceil_paged_copy(const uint64_t* src_k, const uint64_t* src_v, con
   if (grid_x((n_tokens + p.tile_tokens - 1) / p.tile_tokens, &gx) != 0) return 1;
   hipLaunchKernelGGL(paged_copy_kernel, dim3(gx, static_cast<unsigned>(layers)), dim3(128), 0,
                      static_cast<hipStream_t>(stream), p);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// As ceil_paged_copy; kv_split 1 moves K and V by separate waves, and a non-NULL k_read
+// (device, 16 zero words) holds each K store behind one dependent read of it.
+extern "C" int ceil_paged_copy_ex(const uint64_t* src_k, const uint64_t* src_v,
+                                  const uint64_t* dst_k, const uint64_t* dst_v, int32_t layers,
+                                  const int32_t* src_table, int64_t src_table_len,
+                                  int64_t src_blocks, const int32_t* dst_table,
+                                  int64_t dst_table_len, int64_t dst_blocks, int64_t n_tokens,
+                                  int32_t heads, int32_t row_bytes, int64_t s_block,
+                                  int64_t s_head, int64_t s_off, int64_t d_block, int64_t d_head,
+                                  int64_t d_off, int32_t kv_split, const uint32_t* k_read,
+                                  void* stream) {
+  PagedCopy p;
+  if (paged_args(p, src_k, src_v, dst_k, dst_v, layers, src_table, src_table_len, src_blocks,
+                 dst_table, dst_table_len, dst_blocks, n_tokens, heads, row_bytes, s_block, s_head,
+                 s_off, d_block, d_head, d_off) != 0)
+    return 1;
+  const int rpw = p.rows_per_wave;
+  if (heads % rpw != 0) return 1;
+  if ((rpw - 1) * (s_head > d_head ? s_head : d_head) + row_bytes >= (int64_t{1} << 31)) return 1;
+  const int rows = 2 * rpw;  // two row groups
+  p.tile_tokens = rows / heads > 0 ? rows / heads : 1;
+  if (p.tile_tokens * heads != rows) return 1;  // a tile is whole tokens
+  unsigned gx = 0;
+  if (grid_x((n_tokens + p.tile_tokens - 1) / p.tile_tokens, &gx) != 0) return 1;
+  const dim3 grid(gx, static_cast<unsigned>(layers));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (kv_split && k_read)
+    hipLaunchKernelGGL((paged_copy_ex_kernel<true, true>), grid, dim3(256), 0, st, p, k_read);
+  else if (kv_split)
+    hipLaunchKernelGGL((paged_copy_ex_kernel<true, false>), grid, dim3(256), 0, st, p, k_read);
+  else if (k_read)
+    hipLaunchKernelGGL((paged_copy_ex_kernel<false, true>), grid, dim3(128), 0, st, p, k_read);
+  else
+    hipLaunchKernelGGL((paged_copy_ex_kernel<false, false>), grid, dim3(128), 0, st, p, k_read);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

@@ -3,7 +3,8 @@ to: the stream copy byte for byte with either store policy and by a persistent g
 and the paged copy every row
 of positions [0, n) through both block tables -- bf16 from K/V planes, fp8 from fused
 rows, into an HND cache -- leaving every other row untouched, with a wave's rows in one
-token (8 heads) or each lane resolving its own row (1, 2 or 8 heads, either store)."""
+token (8 heads) or each lane resolving its own row (1, 2 or 8 heads, either store), and
+with K and V in separate waves or K's store held behind a dependent table read."""
 
 from __future__ import annotations
 
@@ -30,6 +31,8 @@ def _lib():
                                     i32, i64, i64, i64, i64, i64, i64, vp]
     lib.ceil_paged_copy_lanes.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
                                           i32, i32, i64, i64, i64, i64, i64, i64, i32, vp]
+    lib.ceil_paged_copy_ex.argtypes = [vp, vp, vp, vp, i32, vp, i64, i64, vp, i64, i64, i64,
+                                       i32, i32, i64, i64, i64, i64, i64, i64, i32, vp, vp]
     return lib
 
 
@@ -62,8 +65,10 @@ def test_stream_copy_persistent(gpu, wgs, nbytes):
 
 
 # (heads, lanes): lanes None = ceil_paged_copy, 0 / 1 = ceil_paged_copy_lanes with nt /
-# sc1 nt stores
-CASES = [(8, None), (8, 0), (8, 1), (2, 1), (1, 0), (1, 1)]
+# sc1 nt stores, "split" / "read" / "split_read" = ceil_paged_copy_ex with K and V in
+# separate waves, K behind a table read, or both
+CASES = [(8, None), (8, 0), (8, 1), (2, 1), (1, 0), (1, 1), (8, "split"), (8, "read"),
+         (8, "split_read")]
 
 
 @pytest.mark.parametrize("heads,lanes", CASES)
@@ -88,11 +93,17 @@ def test_paged_copy(gpu, dtype, heads, lanes):
     args = (s_k, s_v, d_k, d_v, wl.layers, st_dev.data_ptr(), st.size, src_blocks,
             dt_dev.data_ptr(), dt.size, dst_blocks, n, heads, d * eb,
             *[x * eb for x in wl.src.strides], *[x * eb for x in wl.dst.strides])
-    if lanes is None:
-        rc = lib.ceil_paged_copy(*args, None)
-    else:
-        rc = lib.ceil_paged_copy_lanes(*args, lanes, None)
-    assert rc == 0
+    zeros = torch.zeros(16, dtype=torch.int32, device=gpu)
+
+    def call(a):
+        if lanes is None:
+            return lib.ceil_paged_copy(*a, None)
+        if isinstance(lanes, str):
+            return lib.ceil_paged_copy_ex(*a, int("split" in lanes),
+                                          zeros.data_ptr() if "read" in lanes else None, None)
+        return lib.ceil_paged_copy_lanes(*a, lanes, None)
+
+    assert call(args) == 0
     torch.cuda.synchronize(gpu)
     pos = np.arange(n)
     for layer in range(wl.layers):
@@ -104,7 +115,4 @@ def test_paged_copy(gpu, dtype, heads, lanes):
         assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), f"layer {layer}"
     # tables shorter than the positions need are refused
     short = (*args[:6], 2, *args[7:])
-    if lanes is None:
-        assert lib.ceil_paged_copy(*short, None) == 1
-    else:
-        assert lib.ceil_paged_copy_lanes(*short, lanes, None) == 1
+    assert call(short) == 1
