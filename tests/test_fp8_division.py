@@ -73,6 +73,12 @@ def test_scales_by_how_their_reciprocal_rounds(checker):
     assert out.count("scale ") == 7
 
 
+def test_both_ends_of_the_scale_range(checker):
+    # the quotient is correctly rounded for K scales in [2^-90, 2^100]: walk both ends
+    out = _run(checker, _hex([2.0 ** -90, 1.7 * 2.0 ** -90, 1.9 * 2.0 ** 99, 2.0 ** 100]))
+    assert out.count("scale ") == 4
+
+
 def test_the_walk_finds_a_wrong_quotient(checker):
     # planted mistake: RN(y * r) with no correction is one ulp off for many y
     out = subprocess.run([checker, "plain", *_hex([0.1])], capture_output=True, text=True,

@@ -87,7 +87,10 @@ def test_decode_every_code(probe, gpu):
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
-@pytest.mark.parametrize("scale", [0.01, 0.037, 0.081, 0.1])
+# workload-like scales, an exact reciprocal (0.125), RN(1/s) above 1/s (3.0), and both
+# ends of the range the division is correctly rounded over (2^-90 .. 2^100)
+@pytest.mark.parametrize("scale", [0.01, 0.037, 0.081, 0.1, 0.125, 3.0, 2.0 ** -90,
+                                   1.7 * 2.0 ** -60, 1.9 * 2.0 ** 99])
 def test_requantise_lands_exactly_on_and_around_midpoints(probe, gpu, scale):
     """y chosen so that y / scale sits on, or one fp32 step from, every midpoint: the
     division and the encoder together must give the correctly rounded code."""
@@ -95,7 +98,11 @@ def test_requantise_lands_exactly_on_and_around_midpoints(probe, gpu, scale):
     s = np.float32(scale)
     target = _interesting_values()
     target = target[np.isfinite(target)]
-    y = (target.astype(np.float64) * np.float64(s)).astype(np.float32)
+    with np.errstate(over="ignore"):
+        y = (target.astype(np.float64) * np.float64(s)).astype(np.float32)
+    # a shift's y is at most 2 * 448 * s in magnitude, never infinite: the quotient is
+    # defined for finite y only
+    y = y[np.isfinite(y)]
     y = np.concatenate((y, np.nextafter(y, np.float32(-1e9)), np.nextafter(y, np.float32(1e9)),
                         np.random.default_rng(1).standard_normal(20000).astype(np.float32) * 20,
                         np.array([np.nan, 0.0, -0.0], np.float32)))
