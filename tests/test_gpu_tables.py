@@ -13,6 +13,9 @@ in the first half and ``RN(0 * c + 1 * s) = s`` in the second -- the span's cos 
 of every frequency, exactly.  One single-token span per delta, every path writing its own
 flat destination.  (shift_kernels.py:73-84 for the tables; the exact values are pinned
 against float64 closed forms and torch in tests/test_oracle.py.)
+
+Beyond that range (shifts of up to 2^24 positions), 300,000 seeded deltas per theta
+compare the plan pass with the host tables.
 """
 
 from __future__ import annotations
@@ -72,3 +75,28 @@ def test_plan_small_and_host_tables_agree_for_every_delta(gpu, theta):
         print(f"  {name}: {bad.size} of {n} deltas differ from the host tables", flush=True)
         assert bad.size == 0, (f"{name}: deltas {deltas[bad[:10]].tolist()} differ from the "
                                "host tables")
+
+
+@pytest.mark.parametrize("theta", [1e4, 1e6])
+def test_plan_and_host_tables_agree_for_far_deltas(gpu, theta):
+    inv = inv_freq_for(D, theta)
+    rng = np.random.default_rng(int(theta))
+    mag = rng.integers(LIM + 1, 2 ** 24 + 1, size=300000)
+    deltas = mag * rng.choice(np.array([-1, 1]), size=mag.size)
+    n = deltas.size
+    src = torch.zeros(1, HEADS, 2 * D, dtype=torch.float32, device=gpu)
+    src[0, :, : D // 2] = 1.0
+    dst = torch.zeros(n, HEADS, 2 * D, dtype=torch.float32, device=gpu)
+    print(f"case far tables theta={theta}: two-launch, {n} spans", flush=True)
+    plan = ShiftPlan(span_array(_rows(deltas, 0)), CacheSet([src], "flat"), CacheSet([dst], "flat"),
+                     inv_freq=inv, src_mode="flat", dst_mode="flat", direct=False)
+    plan.launch()
+    torch.cuda.synchronize(gpu)
+    host = span_tables(deltas, inv, D)
+    want = np.concatenate((host[:, 0, : D // 2], host[:, 1, D // 2:]), axis=1).view(np.uint32)
+    got = dst[:, :, :D].cpu().numpy()
+    assert np.array_equal(got[:, 0], got[:, 1])
+    got = got[:, 0].view(np.uint32)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    print(f"  {bad.size} of {n} deltas differ from the host tables", flush=True)
+    assert bad.size == 0, deltas[bad[:10]].tolist()
