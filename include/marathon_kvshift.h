@@ -13,8 +13,10 @@
  * rounds K back to the cache element type (RNE), copies V bit for bit, and writes the
  * row at its destination slot (block = slot / block_size, offset = slot % block_size).
  * Dimensions at or above `rotary`, and every element of a delta == 0 span, are copied
- * bit for bit.  cos/sin are the fp32-rounded values of the exact cosine and sine of the
- * fp32 angle (evaluated in double precision on the device).
+ * bit for bit.  cos/sin are the cosine and sine of the fp32 angle evaluated in double
+ * precision and rounded to fp32, by one routine for the device and the host
+ * (marathon_amd/csrc/rope_angle.h; mkv_rope_tables below), so every path's tables hold
+ * the same bits.
  *
  * Conventions shared by every entry point:
  *   - All pointers named "device" are HIP device addresses; nothing is allocated and
@@ -293,12 +295,25 @@ int mkv_shift_spans_noalloc(const mkv_shift_desc_t* desc, void* stream);
 /* Workspace bytes mkv_shift_spans needs for these sizes (-1 on negative input). */
 int64_t mkv_shift_workspace_size(int64_t total_tokens, int32_t n_spans, int32_t rotary);
 
+/*
+ * Host function (no GPU call): the rotation tables of n_spans deltas, [n_spans][2][rotary]
+ * fp32 in the span_tables layout (the cos of each element's angle, then its signed sine),
+ * evaluated by the very routine the plan pass and the small path run on the device
+ * (double-precision reduction and series in IEEE operations, marathon_amd/csrc/
+ * rope_angle.h), so the direct path's tables and the device's are the same bits by
+ * construction.  Replaces the reference's torch cos/sin table build
+ * (shift_kernels.py:73-84) for callers that want this library's tables on the host.
+ * inv_freq: host fp32 [rotary / 2]; deltas: host int32 [n_spans].
+ */
+int mkv_rope_tables(const int32_t* deltas, int32_t n_spans, const float* inv_freq,
+                    int32_t rotary, float* tables);
+
 /* Human-readable reason for the last non-MKV_OK return on this thread ("" if none). */
 const char* mkv_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. */
 int32_t mkv_abi_version(void);
-#define MKV_ABI_VERSION ((3 << 16) | 3)
+#define MKV_ABI_VERSION ((3 << 16) | 4)
 
 #ifdef __cplusplus
 }

@@ -45,7 +45,7 @@ MKV_MAX_HEAD_SIZE = 512
 MKV_DIRECT_MAX_SPANS = 63
 MKV_SMALL_MAX_SPANS = 8
 MKV_SMALL_MAX_INDEX = 64
-MKV_ABI_VERSION = (3 << 16) | 3
+MKV_ABI_VERSION = (3 << 16) | 4
 MKV_ORDER_NONE = 0
 MKV_ORDER_DST_PAGE = 1
 MKV_NOALLOC_SCRATCH_BYTES = 16 << 20
@@ -65,6 +65,7 @@ EXPORTED = (
     "mkv_shift_spans_noalloc",
     "mkv_shift_spans_small",
     "mkv_shift_workspace_size",
+    "mkv_rope_tables",
     "mkv_last_error",
     "mkv_abi_version",
 )
@@ -176,6 +177,9 @@ def _bind(cdll: ctypes.CDLL) -> ctypes.CDLL:
     f = cdll.mkv_shift_workspace_size
     f.restype = ctypes.c_int64
     f.argtypes = [i64, i32, i32]
+    f = cdll.mkv_rope_tables
+    f.restype = ctypes.c_int
+    f.argtypes = [vp, i32, vp, i32, vp]
     cdll.mkv_last_error.restype = ctypes.c_char_p
     cdll.mkv_last_error.argtypes = []
     cdll.mkv_abi_version.restype = ctypes.c_int32
@@ -213,3 +217,24 @@ def check(rc: int) -> None:
     if rc != MKV_OK:
         msg = lib().mkv_last_error().decode(errors="replace")
         raise KVShiftError(rc, msg)
+
+
+def rope_tables(deltas, inv_freq, rotary: int):
+    """``mkv_rope_tables``: the rotation tables of ``deltas`` on the host, fp32
+    ``[n_spans, 2, rotary]``, from the routine the device's tables come from.
+    ``inv_freq``: fp32 ``[rotary / 2]`` (numpy or a CPU tensor)."""
+    import numpy as np
+
+    d = np.ascontiguousarray(np.asarray(deltas), dtype=np.int64)
+    if d.size and (d.min() < -2**31 or d.max() >= 2**31):
+        raise ValueError("deltas outside int32")
+    d = d.astype(np.int32)
+    inv = np.ascontiguousarray(np.asarray(inv_freq, dtype=np.float32).reshape(-1))
+    out = np.zeros((d.size, 2, rotary), np.float32)
+    if rotary == 0 or d.size == 0:
+        return out
+    if inv.size < rotary // 2:
+        raise ValueError(f"inv_freq has {inv.size} entries for rotary {rotary}")
+    check(lib().mkv_rope_tables(d.ctypes.data, d.size, inv.ctypes.data, rotary,
+                                out.ctypes.data))
+    return out

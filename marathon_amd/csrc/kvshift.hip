@@ -54,6 +54,7 @@
 
 #include "fp8_e4m3.h"
 #include "marathon_kvshift.h"
+#include "rope_angle.h"
 
 #pragma clang fp contract(off)
 
@@ -644,14 +645,11 @@ __device__ __forceinline__ uint32_t order_bucket(const TokRec& r, int shift) {
 
 // cos and sin of frequency f's angle for one delta: the fp32 angle fl32(delta * inv_freq[f])
 // (shift_kernels.py:73), its sine and cosine evaluated in double precision and rounded
-// once to fp32.  The one routine behind every table the device makes (the plan pass and
-// the small path), so they hold the same bits.
+// once to fp32 (rope_angle.h).  Every table the device makes (the plan pass and the small
+// path) and every table the host makes (mkv_rope_tables) comes from that one routine, so
+// they hold the same bits.
 __device__ __forceinline__ void angle_cos_sin(int delta, float inv_freq_f, float& c, float& s) {
-  const float ang = static_cast<float>(delta) * inv_freq_f;
-  double sd, cd;
-  sincos(static_cast<double>(ang), &sd, &cd);
-  c = static_cast<float>(cd);
-  s = static_cast<float>(sd);
+  mkv_rope::angle_cos_sin(delta, inv_freq_f, c, s);
 }
 
 // A span's table in the layout every path reads: [2][rotary], the cos of each element's
@@ -1693,6 +1691,28 @@ int scratch_of(hipStream_t st, void** out) {
 extern "C" const char* mkv_last_error(void) { return g_err; }
 
 extern "C" int32_t mkv_abi_version(void) { return MKV_ABI_VERSION; }
+
+extern "C" int mkv_rope_tables(const int32_t* deltas, int32_t n_spans, const float* inv_freq,
+                               int32_t rotary, float* tables) {
+  if (n_spans < 0 || rotary < 0 || rotary % 2 != 0)
+    return fail(MKV_ERR_ARG, "n_spans %d, rotary %d", n_spans, rotary);
+  if (n_spans == 0 || rotary == 0) return MKV_OK;
+  if (deltas == nullptr || inv_freq == nullptr || tables == nullptr)
+    return fail(MKV_ERR_ARG, "null pointer");
+  const int half = rotary / 2;
+  for (int32_t sp = 0; sp < n_spans; ++sp) {
+    float* t = tables + static_cast<int64_t>(sp) * 2 * rotary;
+    for (int f = 0; f < half; ++f) {
+      float c, sn;
+      mkv_rope::angle_cos_sin(deltas[sp], inv_freq[f], c, sn);
+      t[f] = c;
+      t[f + half] = c;
+      t[rotary + f] = -sn;
+      t[rotary + f + half] = sn;
+    }
+  }
+  return MKV_OK;
+}
 
 extern "C" int64_t mkv_shift_workspace_size(int64_t total_tokens, int32_t n_spans,
                                             int32_t rotary) {

@@ -90,9 +90,10 @@ def rope_shift(delta: int, head_size: int, inv_freq: torch.Tensor, device,
                tables: str = "exact") -> RopeShift:
     """Tables that move RoPE'd keys ``delta`` positions (shift_kernels.py:68-84).
 
-    ``tables="exact"`` (the default): cos/sin are the exact values of the fp32 angles
-    ``fl32(delta * inv_freq)`` rounded once to fp32 -- the same numbers the kernel
-    computes on the device.  ``tables="reference"``: the reference's own tables, built
+    ``tables="exact"`` (the default): cos/sin of the fp32 angles ``fl32(delta *
+    inv_freq)`` evaluated in double precision and rounded once to fp32, by the library's
+    host routine (``mkv_rope_tables``) -- the routine the kernels run on the device, so
+    the same bits.  ``tables="reference"``: the reference's own tables, built
     as its ``rope_shift`` builds them, with torch's fp32 ``cos``/``sin`` on ``device``;
     through :func:`scatter_shifted` these reproduce the reference's torch path
     (shift_kernels.py:141-159) bit for bit.
@@ -105,9 +106,10 @@ def rope_shift(delta: int, head_size: int, inv_freq: torch.Tensor, device,
     if tables == "reference":
         return _reference_tables(delta, head_size, inv_freq, device, rotary)
     inv = inv_freq.detach().to(device="cpu", dtype=torch.float32).numpy()
-    ang = (np.float32(delta) * inv).astype(np.float64)
-    c = np.cos(ang).astype(np.float32)
-    s = np.sin(ang).astype(np.float32)
+    # the library's host routine: the bits the plan pass and the small path compute
+    t = _lib.rope_tables([int(delta)], inv, rotary)[0]  # [2, rotary]: cos, signed sine
+    c = t[0, :half].copy()
+    s = t[1, half:].copy()
     emb_c = np.concatenate((c, c))
     emb_s = np.concatenate((s, s))
     cos = np.ones(head_size, np.float32)

@@ -735,20 +735,15 @@ class SmallShifts:
 def span_tables(deltas, inv_freq: torch.Tensor | None, rotary: int) -> np.ndarray:
     """Per-span rotation tables, fp32 ``[n_spans, 2, rotary]``: the cos of each element's
     angle, then its signed sine (-sin on the first half, +sin on the second), where the
-    angle of frequency f is ``fl32(fl32(delta) * inv_freq[f])`` and cos/sin are its exact
-    values rounded once to fp32 (evaluated in float64) -- the tables the plan pass
-    computes on the device (shift_kernels.py:68-84 for the layout)."""
+    angle of frequency f is ``fl32(fl32(delta) * inv_freq[f])`` and cos/sin are evaluated
+    in double precision and rounded once to fp32 by the library's host routine
+    (``mkv_rope_tables``), the one the plan pass runs on the device: the direct path's
+    tables and the device's are the same bits (shift_kernels.py:68-84 for the layout)."""
     deltas = np.asarray(deltas, dtype=np.int64)
-    out = np.zeros((deltas.size, 2, rotary), np.float32)
     if rotary == 0 or deltas.size == 0:
-        return out
+        return np.zeros((deltas.size, 2, rotary), np.float32)
     inv = inv_freq.detach().to(device="cpu", dtype=torch.float32).numpy().reshape(-1)
-    ang = deltas.astype(np.float32)[:, None] * inv[None, :]  # fp32 products, rounded once
-    c = np.cos(ang.astype(np.float64)).astype(np.float32)
-    sn = np.sin(ang.astype(np.float64)).astype(np.float32)
-    out[:, 0, :] = np.concatenate((c, c), axis=1)
-    out[:, 1, :] = np.concatenate((-sn, sn), axis=1)
-    return out
+    return _lib.rope_tables(deltas, inv, rotary)
 
 
 def dst_page_order(spans: np.ndarray, dst: CacheSet, mode: str, index,
