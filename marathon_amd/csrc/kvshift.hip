@@ -93,8 +93,9 @@
 // rotation table in LDS with one 16-byte load per lane, and every lane reads its chunk's
 // cos/sin from there, instead of each lane loading its own 2 x C floats from the table
 // in memory: one global load per lane where fp8's chunk of 16 elements took eight.
-// Bit 1: fp8 (measured 1.3-3% faster on the fp8 Qwen3-14B shift); bit 2: 2-byte
-// elements (four loads per lane before; within the spread, so off).
+// Bit 1: fp8 (measured 1.4-3% faster on the fp8 Qwen3-14B shift); bit 2: 2-byte
+// elements (four loads per lane before: one-span shifts 0.3-1.7% faster, the 8-span
+// Qwen3-14B shift 0.2% slower, so off).
 #ifndef MKV_TABLE_LDS
 #define MKV_TABLE_LDS 1
 #endif
