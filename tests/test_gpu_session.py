@@ -490,17 +490,23 @@ def test_block_store_fp8_saves_and_loads_match_oracle(gpu):
     out = {name: torch.zeros_like(c) for name, c in kv.items()}
     loader = ShiftLoader(store, BS, inv_freq_for(D, 1e6), k_scales=scales)
     loader.register_kv_caches(out)
-    dst_blocks = torch.randperm(64).tolist()
-    assert loader.start_load_kv([Load.from_blocks("a", dst_blocks, 60, 60 + 330, 51)]) == 330 * 3
-    torch.cuda.synchronize(gpu)
     inv = inv_freq_for(D, 1e6).numpy()
-    for name, cache in out.items():
-        s = slots(dst_blocks, 60, 390, BS).to(gpu)
-        got = cache[s // BS, :, s % BS].cpu().view(torch.uint8).numpy()
-        src = store.read("a", name, 9, 330).cpu().view(torch.uint8).numpy()
-        want_k = orc.rotate_k_bits(src[..., :D], 51, inv, "fp8", scales[name])
-        assert np.array_equal(got[..., :D], want_k), name
-        assert np.array_equal(got[..., D:], src[..., D:]), name
+    # the second load runs after a scale changed in the shared dict: the loader's cached
+    # scale tensor must follow it
+    for step, delta in enumerate((51, 23)):  # sources at 9 and 37, inside the saved [3, 403)
+        if step:
+            scales["l1"] = 0.071
+        dst_blocks = torch.randperm(64).tolist()
+        load = Load.from_blocks("a", dst_blocks, 60, 60 + 330, delta)
+        assert loader.start_load_kv([load]) == 330 * 3
+        torch.cuda.synchronize(gpu)
+        for name, cache in out.items():
+            s = slots(dst_blocks, 60, 390, BS).to(gpu)
+            got = cache[s // BS, :, s % BS].cpu().view(torch.uint8).numpy()
+            src = store.read("a", name, 60 - delta, 330).cpu().view(torch.uint8).numpy()
+            want_k = orc.rotate_k_bits(src[..., :D], delta, inv, "fp8", scales[name])
+            assert np.array_equal(got[..., :D], want_k), (step, name)
+            assert np.array_equal(got[..., D:], src[..., D:]), (step, name)
 
 
 def test_deferred_per_layer_saves_equal_one_save_all(gpu):
