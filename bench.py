@@ -629,7 +629,9 @@ def size_sweep(dev, steps: int, warmup: int, stream) -> dict:
     """Informational: one batched shift of n tokens x 40 layers (a flat store span into
     an HND paged cache through shuffled slots, delta 186) for n from 512 to 32,768: how
     the fixed costs of a call (the plan kernel, two launches, ramp-up and drain) weigh
-    on small shifts."""
+    on small shifts.  Beside each: the same bytes through the hand-written stream copy
+    and the same rows through the hand-written paged copy (one block id per token, then
+    the data), each one launch timed the same way."""
     import numpy as np
     import torch
 
@@ -665,16 +667,59 @@ def size_sweep(dev, steps: int, warmup: int, stream) -> dict:
         st = ctypes.c_void_p(stream.cuda_stream)
         cms = _time_launch(lambda: cl.ceil_stream_copy(a.data_ptr(), b.data_ptr(), half, 1, st),
                            max(steps, 50), stream)
+        del a, b
+        pms = _sweep_paged_copy(cl, plan, table, n, max(steps, 50), stream)
+        moved = plan.algorithmic_bytes
         out[f"tokens_{n}"] = {"ms": round(ms, 4), "GB_s": round(gbs, 1),
                               "frac_of_peak": round(gbs / PEAK_GBS, 4),
                               "us_per_token": round(ms * 1e3 / n, 5),
                               "stream_copy_ms": round(cms, 4),
                               "stream_copy_frac_of_peak": round(
-                                  plan.algorithmic_bytes / (cms / 1e3) / 1e9 / PEAK_GBS, 4)}
-        del a, b
+                                  moved / (cms / 1e3) / 1e9 / PEAK_GBS, 4),
+                              "paged_copy_ms": round(pms, 4),
+                              "paged_copy_frac_of_peak": round(
+                                  moved / (pms / 1e3) / 1e9 / PEAK_GBS, 4)}
         del src, kv, plan
         torch.cuda.empty_cache()
     return out
+
+
+def _sweep_paged_copy(cl, plan, table, n: int, runs: int, stream) -> float:
+    """The size sweep's rows (n tokens x every layer, the flat source read as 16-token
+    blocks in order, the destination through the sweep's block table) moved by the
+    hand-written paged copy, which reads one block id per token and then the data, with
+    no rotation and no span or slot metadata.  Returns the median ms of ``runs``
+    launches, after checking eight sampled rows."""
+    import torch
+
+    dev = plan.dst.first.device
+    eb = plan.dst.first.element_size()
+    heads, d, layers = plan.dst.heads, plan.dst.head_size, plan.dst.layers
+    s_k, s_v, _, _, _ = plan.src.device_tables(dev)
+    d_k, d_v, _, _, _ = plan.dst.device_tables(dev)
+    row, s_head, _ = plan.src.strides  # flat rows: token stride, head stride
+    d_block, d_head, d_off = plan.dst.strides
+    ident = torch.arange(n // 16, dtype=torch.int32, device=dev)
+    tab = table.to(torch.int32)
+    torch.cuda.synchronize()
+    st = ctypes.c_void_p(stream.cuda_stream)
+    args = (s_k, s_v, d_k, d_v, layers, ident.data_ptr(), ident.numel(), n // 16,
+            tab.data_ptr(), tab.numel(), plan.dst.first.shape[0], n, heads, d * eb,
+            16 * row * eb, s_head * eb, row * eb, d_block * eb, d_head * eb, d_off * eb, st)
+
+    def launch():
+        if cl.ceil_paged_copy(*args) != 0:
+            raise RuntimeError("ceil_paged_copy refused the size sweep's arguments")
+
+    ms = _time_launch(launch, runs, stream)
+    for k in range(8):
+        pos, layer = (k * 977 + 5) % n, (k * 13) % layers
+        blk = int(tab[pos // 16])
+        want = plan.src.caches[0][layer][pos]
+        got = plan.dst.caches[0][layer][blk, :, pos % 16]
+        if not torch.equal(want.view(torch.uint8), got.contiguous().view(torch.uint8)):
+            raise AssertionError(f"size sweep paged copy: row {pos} layer {layer}")
+    return ms
 
 
 def ceilings(dev, steps: int, warmup: int, stream) -> dict:
