@@ -165,6 +165,8 @@ def _two_session_plan(gpu, dtype, heads, d, rotary, seed, spans, table, k_scale=
     (torch.bfloat16, 64, 128, 128),      # one token is 8 passes of a workgroup
     (torch.float8_e4m3fn, 8, 64, 64),    # fp8: 16 rows per wave span two tokens
     (torch.float8_e4m3fn, 3, 256, 128),  # fp8: ragged heads, partial rotary
+    (torch.float8_e4m3fn, 8, 128, 64),   # fp8, whole tokens per pass (span table in LDS),
+    (torch.float8_e4m3fn, 8, 256, 128),  # partial rotary
 ])
 def test_batched_other_geometries_match_oracle(gpu, dtype, heads, d, rotary):
     """Non-uniform head counts (a wave pass spans tokens), partial rotary, fp16 / fp32 /
