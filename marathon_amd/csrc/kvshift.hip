@@ -89,6 +89,12 @@
 #ifndef MKV_WG_THREADS
 #define MKV_WG_THREADS 128
 #endif
+// Plan pass: the per-span cos/sin tables are made by workgroups of their own, which need
+// no token prefix, instead of by the first record workgroups after their records' chain
+// (0.5 us less per two-launch call on 2,048-token and one-head shifts; 0: off).
+#ifndef MKV_PLAN_TABLE_GROUPS
+#define MKV_PLAN_TABLE_GROUPS 1
+#endif
 // Record and direct paths with one token per wave pass: each wave stages its span's
 // rotation table in LDS with one 16-byte load per lane, and every lane reads its chunk's
 // cos/sin from there, instead of each lane loading its own 2 x C floats from the table
@@ -302,7 +308,7 @@ struct PlanParams {
   int32_t n_spans;
   int32_t layers;
   int32_t rotary;
-  int32_t pad;
+  int32_t rec_groups;  // workgroups 0 .. rec_groups - 1 resolve records; the rest, tables
   DevSide src;
   DevSide dst;
 };
@@ -678,12 +684,34 @@ __device__ __forceinline__ void put_table(float* t, int rotary, int f, float c, 
 // grid-stride share of the tokens into records and of (span, frequency) pairs into
 // the cos/sin tables.
 
+// cos / signed sin per span, element-indexed like the reference's tables: (span,
+// frequency) pairs from `first` in steps of `stride`
+__device__ __forceinline__ void plan_tables(const PlanParams& p, int64_t first, int64_t stride) {
+  const int half = p.rotary / 2;
+  const int64_t pairs = static_cast<int64_t>(p.n_spans) * half;
+  for (int64_t idx = first; idx < pairs; idx += stride) {
+    const int s = static_cast<int>(idx / half);
+    const int f = static_cast<int>(idx - static_cast<int64_t>(s) * half);
+    float c, sn;
+    angle_cos_sin(p.spans[s].delta, p.inv_freq[f], c, sn);
+    put_table(p.tables + static_cast<int64_t>(s) * 2 * p.rotary, p.rotary, f, c, sn);
+  }
+}
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
   extern __shared__ int64_t s_pre[];  // [n_spans + 1]: exclusive prefix of tokens
   __shared__ int64_t s_part[kPlanThreads];
   __shared__ int s_bad;
   const int tid = threadIdx.x;
   const int n = p.n_spans;
+  const int rec_groups = p.rec_groups;
+#if MKV_PLAN_TABLE_GROUPS
+  if (static_cast<int>(blockIdx.x) >= rec_groups) {  // a table workgroup (uniform)
+    plan_tables(p, static_cast<int64_t>(blockIdx.x - rec_groups) * kPlanThreads + tid,
+                static_cast<int64_t>(gridDim.x - rec_groups) * kPlanThreads);
+    return;
+  }
+#endif
   const bool checker = blockIdx.x == 0 && p.err != nullptr;  // workgroup 0 checks the spans
   if (tid == 0) s_bad = 0;
 
@@ -736,21 +764,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p) {
   __syncthreads();
   const int64_t actual = s_pre[n];
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * kPlanThreads + tid;
-  const int64_t gstride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
+  const int64_t gstride = static_cast<int64_t>(rec_groups) * kPlanThreads;
 
   if (checker && tid == 0 && (s_bad != 0 || actual > p.total_tokens))
     atomicOr(p.err, MKV_FLAG_SPAN);
 
-  // cos / signed sin per span, element-indexed like the reference's tables
-  const int half = p.rotary / 2;
-  const int64_t pairs = static_cast<int64_t>(n) * half;
-  for (int64_t idx = gtid; idx < pairs; idx += gstride) {
-    const int s = static_cast<int>(idx / half);
-    const int f = static_cast<int>(idx - static_cast<int64_t>(s) * half);
-    float c, sn;
-    angle_cos_sin(p.spans[s].delta, p.inv_freq[f], c, sn);
-    put_table(p.tables + static_cast<int64_t>(s) * 2 * p.rotary, p.rotary, f, c, sn);
-  }
+#if !MKV_PLAN_TABLE_GROUPS
+  plan_tables(p, gtid, gstride);
+#endif
 
   // token records: grid-stride, or (ordered) one contiguous chunk per workgroup with
   // its page histogram
@@ -1965,7 +1986,16 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
   pp.rotary = d->rotary;
 
   const int64_t pairs = static_cast<int64_t>(d->n_spans) * (d->rotary / 2);
+#if MKV_PLAN_TABLE_GROUPS
+  // record workgroups for the tokens, then table workgroups for the (span, frequency) pairs
+  const int64_t work = d->total_tokens;
+  int64_t tab_grid = (pairs + kPlanThreads - 1) / kPlanThreads;
+  if (tab_grid > 256) tab_grid = 256;
+#else
+  // every workgroup resolves records, then makes tables
   const int64_t work = d->total_tokens > pairs ? d->total_tokens : pairs;
+  const int64_t tab_grid = 0;
+#endif
   int64_t plan_grid = (work + kPlanThreads - 1) / kPlanThreads;
   if (plan_grid > 4096) plan_grid = 4096;
   if (plan_grid < 1) plan_grid = 1;
@@ -1986,8 +2016,9 @@ int shift_spans(const mkv_shift_desc_t* d, void* stream, bool noalloc) {
     pp.order_shift = shift;
   }
   const size_t lds = sizeof(int64_t) * (static_cast<size_t>(d->n_spans) + 1);
-  hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid)), dim3(kPlanThreads), lds,
-                     st, pp);
+  pp.rec_groups = static_cast<int32_t>(plan_grid);  // the order kernel's groups too
+  hipLaunchKernelGGL(plan_kernel, dim3(static_cast<unsigned>(plan_grid + tab_grid)),
+                     dim3(kPlanThreads), lds, st, pp);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MKV_ERR_HIP, "plan launch failed: %s", hipGetErrorString(e));
   if (ordered) {
