@@ -101,9 +101,10 @@
 // in memory: one global load per lane where fp8's chunk of 16 elements took eight.
 // Bit 1: fp8 (measured 1.4-3% faster on the fp8 Qwen3-14B shift); bit 2: 2-byte
 // elements (four loads per lane before: one-span shifts 0.3-1.7% faster, the 8-span
-// Qwen3-14B shift 0.2% slower, so off).
+// Qwen3-14B shift 0.2% slower, so off); bit 4: fp8 on the per-lane path, where a wave's
+// rows span tokens (one-head to four-head shares 0.3-1.2% faster).
 #ifndef MKV_TABLE_LDS
-#define MKV_TABLE_LDS 1
+#define MKV_TABLE_LDS 5
 #endif
 #ifndef MKV_TABLE_WITH_DATA
 #define MKV_TABLE_WITH_DATA 1
@@ -1055,8 +1056,10 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
   constexpr bool kLdsTab =
       BATCHED && UNIFORM && !SMALL &&
       (((MKV_TABLE_LDS & 1) != 0 && DT == MKV_FP8_E4M3) || ((MKV_TABLE_LDS & 2) != 0 && E::kBytes == 2));
+  constexpr bool kLdsTabLanes =
+      BATCHED && !UNIFORM && !SMALL && (MKV_TABLE_LDS & 4) != 0 && DT == MKV_FP8_E4M3;
   float* wave_tab = nullptr;
-  if constexpr (kLdsTab) {
+  if constexpr (kLdsTab || kLdsTabLanes) {
     __shared__ __align__(16) float tab_lds[kWaves][2 * MKV_MAX_HEAD_SIZE];
     wave_tab = tab_lds[wave];
   }
@@ -1076,6 +1079,29 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     }
   };
   (void)stage_table;
+  // the per-lane path's tables (kLdsTabLanes; the whole wave calls it): `need` lanes
+  // rotate with span `sp` and lack its table.  The wave stages the span of the first such
+  // lane in LDS and every lane needing that span reads it there, then the next span, until
+  // none is left (a wave's rows rarely straddle two spans)
+  auto lane_tables = [&](bool need, int sp) {
+    for (uint64_t needs = __ballot(need); needs != 0; needs = __ballot(need)) {
+      const int sp0 = __builtin_amdgcn_readlane(sp, __builtin_ctzll(needs));
+      const float* tb = p.tables + static_cast<int64_t>(sp0) * 2 * p.rotary;
+      for (int c = lane; c < p.rotary / 2; c += 64)
+        *reinterpret_cast<u32x4*>(wave_tab + 4 * c) = *reinterpret_cast<const u32x4*>(tb + 4 * c);
+      __builtin_amdgcn_wave_barrier();  // a wave's LDS accesses complete in order
+      if (need && sp == sp0) {
+#pragma unroll
+        for (int e = 0; e < C; ++e) {
+          cs[e] = wave_tab[j * C + e];
+          sg[e] = wave_tab[p.rotary + j * C + e];
+        }
+        cur_span = sp;
+        need = false;
+      }
+    }
+  };
+  (void)lane_tables;
   // a single span's cos/sin and fp8's K scales are loaded behind the first pass's data
   // (phase B), not here: they are needed only for the rotation, and a load in flight at
   // the pass loop's head would hold back the first data loads
@@ -1375,7 +1401,10 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
     }
 #endif
 #if MKV_TABLE_WITH_DATA_LANES
-    if constexpr (BATCHED && !UNIFORM) {
+    if constexpr (kLdsTabLanes) {
+      lane_tables(live[0] && lane_live && rot_lane && delta_u[0] != 0 && span_u[0] != cur_span,
+                  span_u[0]);
+    } else if constexpr (BATCHED && !UNIFORM) {
       if (live[0] && lane_live && rot_lane && delta_u[0] != 0 && span_u[0] != cur_span) {
         const float* tb = p.tables + static_cast<int64_t>(span_u[0]) * 2 * p.rotary;
 #pragma unroll
@@ -1456,13 +1485,17 @@ __device__ __forceinline__ void shift_body(const ShiftParams& p, const SmallPack
           cur_span = span_u[u];
         }
       }
+      if constexpr (kLdsTabLanes)
+        lane_tables(MKV_STORES(x) && lane_live && rot_lane && delta_u[u] != 0 &&
+                        span_u[u] != cur_span,
+                    span_u[u]);
       u32x4 pd;
       pd[0] = bpermute(partner_addr, kd[x][0]);
       pd[1] = bpermute(partner_addr, kd[x][1]);
       pd[2] = bpermute(partner_addr, kd[x][2]);
       pd[3] = bpermute(partner_addr, kd[x][3]);
       if (MKV_STORES(x) && lane_live && rot_lane && delta_u[u] != 0) {
-        if constexpr (BATCHED && !kLdsTab) {
+        if constexpr (BATCHED && !kLdsTab && !kLdsTabLanes) {
           if (span_u[u] != cur_span) {
             if constexpr (SMALL) {
               // the workgroup's own table, computed into LDS in phase B
